@@ -1,0 +1,246 @@
+"""Benchmark of the attention forward path on one MI355X; prints ONE JSON line.
+
+    python bench.py                         # N=1: headline C4 + per-config table + CPU baseline
+    python bench.py --steps 50 --warmup 10
+    python bench.py --mode pmc              # short fixed workload for rocprofv3 --pmc runs
+
+A step is one cuda_attn.fused_tc call on the headline workload, C4: non-causal SDPA forward,
+B=4 H=32 N=4096 d=128, bf16 inputs from a seeded generator (synthetic data), already resident in
+HBM. `value` = 4*B*H*N^2*d FLOPs per step x steps / wall time of the K steps between two
+synchronisations (HIP events on the launch stream). Every config of the measurement plan is also
+timed with the reference's protocol (/root/reference/bench/benchmark.py:78-93: warm-ups, then per
+call a flush of a buffer larger than the 256 MB Infinity Cache, event timing, median/p10/p90)
+and reported under "per_config". Before timing, outputs are gated against a float64 GPU reference
+on sampled heads. The CPU baseline is the oracle's NumPy restatement of the reference's online
+softmax (oracle/online_softmax.py, br=64 bc=32, P rounded to bf16) timed on a bounded sample of C4.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "phantom-a100_amd"))
+
+import cuda_attn  # noqa: E402
+from cuda_attn import _native  # noqa: E402
+from cuda_attn.workloads import CONFIGS, config_inputs  # noqa: E402
+
+METRIC = "attention fwd TFLOP/s + % of MFMA/HBM roofline per config, 1 MI355X"
+HEADLINE = "C4"
+# MI355X published dense peaks (TFLOP/s) and HBM3E bandwidth (GB/s).
+PEAK_TFLOPS = {torch.bfloat16: 2500.0, torch.float16: 2500.0, torch.float32: 157.3}
+PEAK_HBM_GBS = 8000.0
+DTYPE_NAME = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fa_mfma_C4.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def entry_call(cfg, q, k, v, out_dtype=None):
+    od = cfg.out_dtype if out_dtype is None else out_dtype
+    if cfg.entry == "fused":
+        return lambda: cuda_attn.fused(q, k, v, out_dtype=od)
+    return lambda: cuda_attn.fused_tc(q, k, v, out_dtype=od)
+
+
+def gate(cfg, q, k, v, fn) -> float:
+    """Max abs error of the config's output (fp32 output) on sampled heads vs float64 on the GPU."""
+    out = entry_call(cfg, q, k, v, torch.float32)()
+    heads = sorted({0, cfg.BH // 2, cfg.BH - 1})
+    qh, kh, vh, oh = (t.reshape(cfg.BH, cfg.N, cfg.d)[heads] for t in (q, k, v, out))
+    s = torch.matmul(qh.double(), kh.double().transpose(1, 2).contiguous()) / (cfg.d ** 0.5)
+    ref = torch.matmul(torch.softmax(s, dim=-1), vh.double())
+    return (oh.double() - ref).abs().max().item()
+
+
+def time_steps(fn, steps: int, warmup: int):
+    """Warm-up, then EXACTLY `steps` back-to-back calls bracketed by synchronisations; events on
+    the stream the kernel is launched on (torch's current stream)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1), wall * 1e3
+
+
+def time_reference_protocol(fn, flush, warmup=10, iters=100):
+    """/root/reference/bench/benchmark.py:78-93 with a flush buffer larger than the Infinity Cache."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        flush.zero_()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    times.sort()
+    qs = statistics.quantiles(times, n=10)
+    return statistics.median(times), qs[0], qs[-1]
+
+
+def per_config(flush, iters: int):
+    rows = {}
+    for name, cfg in CONFIGS.items():
+        q, k, v = config_inputs(cfg, device="cuda")
+        fn = entry_call(cfg, q, k, v)
+        err = gate(cfg, q, k, v, fn)
+        med, p10, p90 = time_reference_protocol(fn, flush, iters=iters)
+        tf = cfg.flops() / (med * 1e-3) / 1e12
+        gbs = cfg.hbm_bytes() / (med * 1e-3) / 1e9
+        rows[name] = {
+            "shape": [cfg.B, cfg.H, cfg.N, cfg.d], "dtype": DTYPE_NAME[cfg.dtype], "out_dtype": DTYPE_NAME[cfg.out_dtype],
+            "entry": cfg.entry, "median_ms": round(med, 5), "p10_ms": round(p10, 5), "p90_ms": round(p90, 5),
+            "tflops": round(tf, 3), "pct_mfma_peak": round(100 * tf / PEAK_TFLOPS[cfg.dtype], 3),
+            "achieved_GBps": round(gbs, 1), "pct_hbm_bw": round(100 * gbs / PEAK_HBM_GBS, 3),
+            "max_abs_err_vs_f64": float(f"{err:.3e}"),
+        }
+        log(f"[per-config] {name}: {med:.4f} ms  {tf:.1f} TFLOP/s  err={err:.2e}")
+        del q, k, v
+    return rows
+
+
+def cpu_baseline(cfg, budget_s: float):
+    """Time the oracle's NumPy online softmax (the reference's CPU path) on whole heads of cfg."""
+    import numpy as np
+    import oracle
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    q, k, v = (t.reshape(cfg.BH, cfg.N, cfg.d) for t in config_inputs(cfg, device="cpu"))
+    p_dtype = {torch.bfloat16: "bfloat16", torch.float16: "float16"}.get(cfg.dtype)
+    heads, elapsed = 0, 0.0
+    while heads < cfg.BH and elapsed < budget_s:
+        h = heads
+        qh, kh, vh = (t[h:h + 1].float().numpy() for t in (q, k, v))
+        t0 = time.perf_counter()
+        oracle.attention_online(qh, kh, vh, False, br=64, bc=32, p_dtype=p_dtype)
+        elapsed += time.perf_counter() - t0
+        heads += 1
+    flops = 4.0 * heads * cfg.N * cfg.N * cfg.d
+    return {
+        "value": round(flops / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+        "sample": f"{heads} of {cfg.BH} heads of {cfg.name} (N={cfg.N}, d={cfg.d}) through "
+                  f"oracle.attention_online(br=64, bc=32, p_dtype={p_dtype}) in {elapsed:.1f} s; "
+                  f"NumPy BLAS threads={threads}, host cpus={os.cpu_count()}",
+        "seconds": round(elapsed, 2),
+    }
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            return json.load(fh).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default=HEADLINE, choices=list(CONFIGS))
+    ap.add_argument("--iters", type=int, default=100, help="timed calls per config (reference protocol)")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-per-config", action="store_true")
+    ap.add_argument("--mode", choices=["bench", "pmc"], default="bench")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py: this build measures one GPU; the attention forward path has no multi-GPU "
+            "code (every GPU box here has one GPU). Run with --gpus 1.")
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        log("bench.py: no GPU visible")
+        sys.exit(1)
+    _native.lib()  # fail loudly if the HIP library is missing
+
+    cfg = CONFIGS[args.config]
+    q, k, v = config_inputs(cfg, device="cuda")
+    fn = entry_call(cfg, q, k, v)
+
+    if args.mode == "pmc":
+        # Known-size copy (calibrates FETCH_SIZE / WRITE_SIZE), then a few launches of the kernel.
+        src = torch.ones(256 * 2**20, dtype=torch.float32, device="cuda")   # 1 GiB
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        log(f"pmc workload done: copy {src.numel() * 4} bytes, 3 x {cfg.name}")
+        return
+
+    err = gate(cfg, q, k, v, fn)
+    tol = 1e-5 if cfg.dtype == torch.float32 else 2e-3
+    log(f"[gate] {cfg.name} max abs error vs float64 (sampled heads) = {err:.3e} (tol {tol:.0e})")
+    if not err <= tol:
+        log("bench.py: correctness gate failed; not timing a wrong result")
+        sys.exit(3)
+
+    ms_total, wall_ms = time_steps(fn, args.steps, args.warmup)
+    ms_step = ms_total / args.steps
+    flops = cfg.flops()
+    value = flops * args.steps / (ms_total * 1e-3) / 1e12
+    log(f"[timed] {args.steps} steps: {ms_total:.3f} ms (wall {wall_ms:.3f} ms) -> {value:.1f} TFLOP/s")
+
+    out = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": DTYPE_NAME[cfg.dtype], "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: non-causal SDPA forward B={cfg.B} H={cfg.H} N={cfg.N} d={cfg.d} "
+                               f"{DTYPE_NAME[cfg.dtype]}, Q/K/V ~ N(0,1) (Q,K x{cfg.qk_scale:g}), seed {cfg.seed}, "
+                               f"cuda_attn.{cfg.entry}",
+                   "B": cfg.B, "H": cfg.H, "N": cfg.N, "d": cfg.d, "causal": False, "entry": cfg.entry,
+                   "out_dtype": DTYPE_NAME[cfg.out_dtype]},
+        "roofline": {"bound": "mfma", "achieved": round(flops / (ms_step * 1e-3) / 1e12, 3),
+                     "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s",
+                     "frac": round(flops / (ms_step * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 5),
+                     "traffic": traffic_from_profile() if cfg.name == HEADLINE else None,
+                     "kernel": "pa::fa_mfma_fwd<bf16, D=128, BM=128, BN=64, 2 stages>",
+                     "flops_per_launch": flops},
+        "gate_max_abs_err": float(f"{err:.3e}"),
+        "library": _native.version(),
+        "device": torch.cuda.get_device_name(0),
+    }
+    del q, k, v
+    torch.cuda.empty_cache()
+    if not args.no_per_config:
+        flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")  # > 256 MB Infinity Cache
+        out["per_config"] = per_config(flush, args.iters)
+        del flush
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
+        log(f"[cpu] {out['cpu_baseline']['sample']}: {out['cpu_baseline']['value']} TFLOP/s")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,146 @@
+"""CPU oracle for the attention forward path: TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``
+may import this module, and only as the checker or the timed CPU baseline. The product
+(``cuda_attn`` and its HIP library) never imports or calls it.
+
+It restates, in my own NumPy code, the reference's CPU model of the fused kernels:
+
+* ``attention_naive``  - textbook float64 softmax(QK^T/sqrt(d))V
+  (follows /root/reference/cuda_attn/online_softmax_ref.py:14-24).
+* ``attention_online`` - the tile-by-tile online softmax in the log2 domain, float32
+  (follows /root/reference/cuda_attn/online_softmax_ref.py:27-63): Q pre-scaled by
+  log2(e)/sqrt(d), running max m and sum l per row, alpha = 2^(m - m_new) with the
+  -inf guards, optional rounding of P before the P@V product while l is summed from the
+  unrounded P (v4's rule, /root/reference/csrc/kernels/fused_tc.cuh:150-165).
+  ``p_dtype`` extends the reference's ``p_fp16`` flag to bfloat16.
+* ``attention_f64_rows`` - float64 truth computed in row blocks, for shapes whose full
+  N x N score matrix would not fit in host memory (same math as attention_naive).
+
+How each function is pinned (tests/test_oracle.py): attention_naive against the
+independent C brute force in oracle/attn_ref64.c and closed forms (N=1 -> V, constant
+K -> mean of V, one-hot V -> P, a hand-computed 2x2 case); attention_online against
+attention_naive for the reference's own test matrix (tests/test_algorithm.py:12-46 of
+the reference), tile-size invariance, and an exact-representability check that pins where
+P is rounded; round_bf16 against torch's bfloat16 cast.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+LOG2E = 1.4426950408889634
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bfloat16 (ties to even), returned as float32.
+
+    NumPy has no bfloat16; this keeps the top 16 bits of the float32 pattern after adding
+    the round-to-nearest-even bias. inf stays inf; finite values past the bf16 range become inf.
+    """
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = np.isnan(x)
+    lsb = (u >> np.uint32(16)) & np.uint32(1)
+    r = ((u + np.uint32(0x7FFF) + lsb) & np.uint32(0xFFFF0000)).view(np.float32)
+    if nan.any():
+        r = np.where(nan, np.float32(np.nan), r)
+    return r
+
+
+def round_to(x: np.ndarray, dtype: str | None) -> np.ndarray:
+    """Round float32 values to ``dtype`` ("float16", "bfloat16" or None) and back to float32."""
+    if dtype is None or dtype == "float32":
+        return x
+    if dtype == "float16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype == "bfloat16":
+        return round_bf16(x)
+    raise ValueError(f"unknown rounding dtype {dtype!r}")
+
+
+def attention_naive(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False) -> np.ndarray:
+    """Textbook softmax(QK^T / sqrt(d)) V on (..., N, d) arrays, in float64.
+
+    Follows /root/reference/cuda_attn/online_softmax_ref.py:14-24.
+    """
+    q64, k64, v64 = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    n, d = q64.shape[-2], q64.shape[-1]
+    s = np.matmul(q64, np.swapaxes(k64, -1, -2)) / np.sqrt(d)
+    if causal:
+        s = np.where(np.tril(np.ones((n, n), dtype=bool)), s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.matmul(p, v64)
+
+
+def attention_f64_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False,
+                       rows: int = 512) -> np.ndarray:
+    """attention_naive computed in blocks of ``rows`` query rows (float64, bounded memory).
+
+    The score block per call is (..., rows, N) float64 instead of (..., N, N).
+    """
+    q64, k64, v64 = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    n, d = q64.shape[-2], q64.shape[-1]
+    out = np.empty(q64.shape, dtype=np.float64)
+    kt = np.swapaxes(k64, -1, -2)
+    inv = 1.0 / np.sqrt(d)
+    for i0 in range(0, n, rows):
+        i1 = min(n, i0 + rows)
+        s = np.matmul(q64[..., i0:i1, :], kt) * inv
+        if causal:
+            keep = np.arange(n)[None, :] <= np.arange(i0, i1)[:, None]
+            s = np.where(keep, s, -np.inf)
+        s -= s.max(axis=-1, keepdims=True)
+        np.exp(s, out=s)
+        s /= s.sum(axis=-1, keepdims=True)
+        out[..., i0:i1, :] = np.matmul(s, v64)
+    return out
+
+
+def attention_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False,
+                     br: int = 64, bc: int = 32, p_fp16: bool = False,
+                     p_dtype: str | None = None) -> np.ndarray:
+    """Tile-by-tile online softmax in float32, the way the fused kernels compute it.
+
+    Follows /root/reference/cuda_attn/online_softmax_ref.py:27-63. ``p_fp16=True`` (or
+    ``p_dtype="float16"``) rounds P to float16 before P @ V while l sums the unrounded
+    float32 P; ``p_dtype="bfloat16"`` does the same with bfloat16 (extension for the
+    bf16 MFMA path, which the reference does not have).
+    """
+    if p_fp16:
+        if p_dtype not in (None, "float16"):
+            raise ValueError("p_fp16=True conflicts with p_dtype=%r" % (p_dtype,))
+        p_dtype = "float16"
+    q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
+    *batch, n, d = q32.shape
+    out = np.empty_like(q32)
+    scale_log2 = np.float32(LOG2E / np.sqrt(d))
+    kt = np.swapaxes(k32, -1, -2)
+
+    for i0 in range(0, n, br):                               # one workgroup's query rows
+        i1 = min(i0 + br, n)
+        qi = q32[..., i0:i1, :] * scale_log2                 # log2 domain
+        r = i1 - i0
+        rows = np.arange(i0, i1)
+        m = np.full((*batch, r), -np.inf, np.float32)
+        l = np.zeros((*batch, r), np.float32)
+        o = np.zeros((*batch, r, d), np.float32)
+        kv_end = min(n, i1) if causal else n
+        for j0 in range(0, kv_end, bc):                      # stream K/V tiles
+            j1 = min(j0 + bc, n)
+            s = np.matmul(qi, kt[..., :, j0:j1])
+            if causal:
+                cols = np.arange(j0, j1)
+                s = np.where(cols[None, :] > rows[:, None], np.float32(-np.inf), s)
+            m_new = np.maximum(m, s.max(axis=-1))
+            dead = np.isneginf(m_new)                        # every key so far masked
+            with np.errstate(invalid="ignore"):
+                alpha = np.where(dead, np.float32(0), np.exp2(m - m_new)).astype(np.float32)
+                p = np.where(dead[..., None], np.float32(0),
+                             np.exp2(s - m_new[..., None])).astype(np.float32)
+            l = l * alpha + p.sum(axis=-1, dtype=np.float32)
+            p_mm = round_to(p, p_dtype)
+            o = o * alpha[..., None] + np.matmul(p_mm, v32[..., j0:j1, :])
+            m = m_new
+        out[..., i0:i1, :] = o / l[..., None]
+    return out

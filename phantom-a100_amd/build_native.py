@@ -1,0 +1,76 @@
+"""Build libphantom_attn.so (the HIP kernels + C ABI) for gfx950, in-tree.
+
+    python phantom-a100_amd/build_native.py            # -> phantom-a100_amd/cuda_attn/libphantom_attn.so
+
+hipcc cross-compiles without a GPU. Flags:
+  --offload-arch=gfx950                  MI355X (CDNA4) only
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                         no packed fp32 (v_pk_*_f32) instructions in device code
+  -mllvm -amdgpu-mfma-vgpr-form=1        MFMA accumulators in ordinary VGPRs, so the softmax can
+                                         read S and rescale O without accvgpr copies
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+OUT = os.path.join(HERE, "cuda_attn", "libphantom_attn.so")
+SOURCES = ["pa_attn.hip"]
+ARCH = "gfx950"
+
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+]
+COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result"]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found (ROCm is required to build libphantom_attn.so)")
+    return path
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source and link libphantom_attn.so; returns its path."""
+    objs = []
+    os.makedirs(os.path.join(HERE, "_build"), exist_ok=True)
+    procs = []
+    for src in SOURCES:
+        obj = os.path.join(HERE, "_build", os.path.splitext(src)[0] + ".o")
+        cmd = [hipcc(), *DEVICE_FLAGS, *COMMON_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
+               os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objs.append(obj)
+    failed = []
+    for src, p in procs:
+        out, _ = p.communicate()
+        # hipcc's host pass does not know the device-only target feature; that warning is noise.
+        lines = [ln for ln in out.splitlines() if "unknown target feature" not in ln and ln.strip()
+                 and "packed-fp32-ops" not in ln]
+        if p.returncode != 0:
+            failed.append(src)
+            print("\n".join(lines), file=sys.stderr)
+        elif verbose and lines:
+            print("\n".join(lines))
+    if failed:
+        raise RuntimeError("hipcc failed for: " + ", ".join(failed))
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,83 @@
+// Device-side helpers shared by every attention kernel (gfx950 / CDNA4, wave64).
+//
+// Storage types are the compiler's native _Float16 and __bf16; all softmax arithmetic is fp32.
+// Nothing here depends on PyTorch: the kernels are reached only through the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pa {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+constexpr int kNumXcd = 8;  // MI355X: 8 accelerator complex dies, each with its own L2
+
+// LDS pointer type for builtins that take an address_space(3) operand.
+template <typename T>
+using lds_ptr = __attribute__((address_space(3))) T*;
+
+// Vector of 8 storage elements, the per-lane operand of a K=16 (32x32) / K=32 (16x16) MFMA.
+template <typename T> struct vec8;
+template <> struct vec8<f16> { typedef f16x8 type; };
+template <> struct vec8<bf16> { typedef bf16x8 type; };
+
+// D = A * B + C on a 32x32x16 tile. Lane l holds A[l%32][8*(l/32)+j], B[8*(l/32)+j][l%32] and
+// C[8*(r/4) + 4*(l/32) + r%4][l%32] in register r (layouts checked on the device).
+__device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// fp32 32x32x2: lane l holds A[l%32][l/32], B[l/32][l%32]; C as above.
+__device__ __forceinline__ f32x16 mfma32x32x2(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// All-reduce across the two 32-lane halves of the wave: lane l and lane l^32 both get
+// op(x[l], x[l^32]). v_permlane32_swap(x, x) hands every lane {x[l%32], x[l%32 + 32]}.
+__device__ __forceinline__ float half_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
+                                            false, false);
+  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
+                                            false, false);
+  return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
+}
+
+// 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Storage conversions, round to nearest even.
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+
+// Maps the hardware workgroup id to a logical one so that consecutive logical ids run on the
+// same XCD: the dispatcher sends workgroup g to XCD g % 8, so logical id
+// (g % 8) * (total / 8) + g / 8 keeps a contiguous range of (head, query-block) pairs - the
+// blocks that re-read the same K/V rows - inside one XCD's L2. Identity when total % 8 != 0.
+__device__ __forceinline__ int xcd_remap(int g, int total) {
+  if (total % kNumXcd != 0) return g;
+  return (g % kNumXcd) * (total / kNumXcd) + g / kNumXcd;
+}
+
+}  // namespace pa

@@ -1,0 +1,278 @@
+// C ABI of libphantom_attn.so: argument validation, dispatch to the compiled kernel
+// instantiations, launch on the caller's stream. Declarations and the reference interface each
+// entry replaces are in include/phantom_attn.h.
+//
+// Host-side rules: no allocation, no synchronisation, no per-call hipFuncSetAttribute (all LDS
+// is static, so a launch needs no opt-in call; the reference set the attribute on every call,
+// /root/reference/csrc/kernels/fused_tc.cuh:189-191). Errors come back as status codes with a
+// thread-local message.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+
+#include "phantom_attn.h"
+#include "kernels/fa_f32.hpp"
+#include "kernels/fa_mfma.hpp"
+#include "kernels/unfused.hpp"
+
+#ifndef PA_VERSION_STRING
+#define PA_VERSION_STRING "0.1.0"
+#endif
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* name) {
+  if (e == hipSuccess) return PA_OK;
+  return fail((int)e, "%s: HIP error: %s", name, hipGetErrorString(e));
+}
+
+size_t dtype_bytes(int dt) { return dt == PA_DTYPE_F32 ? 4 : 2; }
+
+// Shared argument checks. Pointers must be non-null and 16-byte aligned (the kernels move
+// 16-byte vectors); sizes must keep every in-kernel 32-bit index in range.
+int check_common(const char* name, const void* q, const void* k, const void* v, const void* o,
+                 int64_t bh, int64_t n, int64_t d) {
+  if (!q || !k || !v || !o) return fail(PA_ERR_INVALID, "%s: null tensor pointer", name);
+  if (bh <= 0 || n <= 0 || d <= 0) return fail(PA_ERR_INVALID, "%s: inputs must be non-empty", name);
+  if (bh > INT_MAX || n > INT_MAX || d > INT_MAX)
+    return fail(PA_ERR_INVALID, "%s: tensor dimension exceeds 2^31-1", name);
+  return PA_OK;
+}
+
+int check_aligned16(const char* name, const void* q, const void* k, const void* v, const void* o) {
+  for (const void* p : {q, k, v, o})
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return fail(PA_ERR_INVALID, "%s: inputs must be 16-byte aligned", name);
+  return PA_OK;
+}
+
+float scale_log2_for(int64_t d) { return pa::kLog2e / sqrtf((float)d); }
+
+// ------------------------------------------------------------------ fused MFMA (fp16 / bf16)
+template <typename T, int D, int BM, int BN, int ST, typename OutT>
+hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int bh, int n, int causal,
+                       hipStream_t stream) {
+  const int qblocks = (n + BM - 1) / BM;
+  const long long total = (long long)qblocks * bh;
+  if (total > INT_MAX) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT>), dim3((unsigned)total), dim3(BM / 32 * pa::kWave), 0,
+                     stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                     static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);
+  return hipGetLastError();
+}
+
+typedef hipError_t (*mfma_fn)(const void*, const void*, const void*, void*, int, int, int, hipStream_t);
+
+struct MfmaEntry {
+  int dtype, out_dtype, d, br, bc, db;
+  mfma_fn fn;
+  int64_t lds;
+};
+
+template <typename T> constexpr int dt_code();
+template <> constexpr int dt_code<pa::f16>() { return PA_DTYPE_F16; }
+template <> constexpr int dt_code<pa::bf16>() { return PA_DTYPE_BF16; }
+template <> constexpr int dt_code<float>() { return PA_DTYPE_F32; }
+
+template <typename T, int D, int BM, int BN, int ST, typename OutT>
+constexpr MfmaEntry mfma_entry() {
+  return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, &launch_mfma<T, D, BM, BN, ST, OutT>,
+                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES};
+}
+
+#define PA_TC_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T>(), mfma_entry<T, D, BM, BN, ST, float>()
+
+// fused_tc: one tile configuration per (dtype, d).
+const MfmaEntry kTcTable[] = {
+    PA_TC_BOTH_OUT(pa::f16, 64, 128, 64, 2),
+    PA_TC_BOTH_OUT(pa::bf16, 64, 128, 64, 2),
+    PA_TC_BOTH_OUT(pa::f16, 128, 128, 64, 2),
+    PA_TC_BOTH_OUT(pa::bf16, 128, 128, 64, 2),
+};
+
+// fused_tuned: the reference's tile sweep set (fused_tuned.cuh:207) x {one, two} LDS stages.
+#define PA_TUNED(BR, BC) PA_TC_BOTH_OUT(pa::f16, 64, BR, BC, 1), PA_TC_BOTH_OUT(pa::f16, 64, BR, BC, 2)
+const MfmaEntry kTunedTable[] = {PA_TUNED(64, 32), PA_TUNED(64, 64), PA_TUNED(128, 32), PA_TUNED(128, 64)};
+
+const MfmaEntry* find_tc(int dtype, int out_dtype, int64_t d) {
+  for (const auto& e : kTcTable)
+    if (e.dtype == dtype && e.out_dtype == out_dtype && e.d == d) return &e;
+  return nullptr;
+}
+const MfmaEntry* find_tuned(int dtype, int out_dtype, int64_t d, int br, int bc, int db) {
+  for (const auto& e : kTunedTable)
+    if (e.dtype == dtype && e.out_dtype == out_dtype && e.d == d && e.br == br && e.bc == bc && e.db == (db ? 1 : 0))
+      return &e;
+  return nullptr;
+}
+
+// ------------------------------------------------------------------ fused fp32 arithmetic
+constexpr int kF32BM = 64, kF32BN = 32;
+
+template <typename T, typename OutT>
+hipError_t launch_f32(const void* q, const void* k, const void* v, void* o, int bh, int n, int causal,
+                      hipStream_t stream) {
+  const int qblocks = (n + kF32BM - 1) / kF32BM;
+  const long long total = (long long)qblocks * bh;
+  if (total > INT_MAX) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((pa::fa_f32_fwd<T, 64, kF32BM, kF32BN, OutT>), dim3((unsigned)total), dim3(kF32BM / 32 * pa::kWave),
+                     0, stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                     static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(64), causal);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ unfused
+template <typename T>
+hipError_t launch_naive(const void* q, const void* k, const void* v, void* o, float* s, int bh, int n, int d,
+                        int causal, hipStream_t stream) {
+  const float scale = 1.f / sqrtf((float)d);
+  hipLaunchKernelGGL(pa::naive_scores<T>, dim3((n + 63) / 64, (n + 3) / 4, bh), dim3(64, 4), 0, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k), s, n, d, scale, causal);
+  hipLaunchKernelGGL(pa::naive_softmax, dim3((n + 255) / 256, bh), dim3(256), 0, stream, s, n);
+  hipLaunchKernelGGL(pa::naive_pv<T>, dim3((d + 63) / 64, (n + 3) / 4, bh), dim3(64, 4), 0, stream, s,
+                     static_cast<const T*>(v), static_cast<T*>(o), n, d);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_tiled(const void* q, const void* k, const void* v, void* o, float* s, int bh, int n, int d,
+                        int causal, hipStream_t stream) {
+  const float scale = 1.f / sqrtf((float)d);
+  const int nt = (n + pa::kTile - 1) / pa::kTile;
+  hipLaunchKernelGGL(pa::tiled_scores<T>, dim3(nt, nt, bh), dim3(256), 0, stream, static_cast<const T*>(q),
+                     static_cast<const T*>(k), s, n, d, scale, causal);
+  hipLaunchKernelGGL(pa::tiled_softmax, dim3((n + 3) / 4, bh), dim3(256), 0, stream, s, n);
+  hipLaunchKernelGGL(pa::tiled_pv<T>, dim3((d + pa::kTile - 1) / pa::kTile, nt, bh), dim3(256), 0, stream, s,
+                     static_cast<const T*>(v), static_cast<T*>(o), n, d, causal);
+  return hipGetLastError();
+}
+
+int unfused_common(const char* name, const void* q, const void* k, const void* v, void* o, const float* s, int dtype,
+                   int64_t bh, int64_t n, int64_t d) {
+  if (int rc = check_common(name, q, k, v, o, bh, n, d)) return rc;
+  if (!s) return fail(PA_ERR_INVALID, "%s: null score workspace", name);
+  if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_F16)
+    return fail(PA_ERR_UNSUPPORTED, "%s: only float32 and float16 are supported", name);
+  if (bh > 65535) return fail(PA_ERR_UNSUPPORTED, "%s: B*H must be at most 65535", name);
+  if ((n + 3) / 4 > 65535) return fail(PA_ERR_UNSUPPORTED, "%s: N must be at most 262140", name);
+  return PA_OK;
+}
+
+// Per-device LDS limit, queried once per device.
+std::mutex g_lds_mu;
+int64_t g_lds_limit[64];
+bool g_lds_known[64];
+
+}  // namespace
+
+extern "C" {
+
+int pa_naive_fwd(const void* q, const void* k, const void* v, void* o, float* s, int dtype, int64_t bh, int64_t n,
+                 int64_t d, int causal, void* stream) {
+  const char* name = "naive_forward";
+  if (int rc = unfused_common(name, q, k, v, o, s, dtype, bh, n, d)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == PA_DTYPE_F32 ? launch_naive<float>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st)
+                                       : launch_naive<pa::f16>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st);
+  return hip_status(e, name);
+}
+
+int pa_tiled_fwd(const void* q, const void* k, const void* v, void* o, float* s, int dtype, int64_t bh, int64_t n,
+                 int64_t d, int causal, void* stream) {
+  const char* name = "tiled_forward";
+  if (int rc = unfused_common(name, q, k, v, o, s, dtype, bh, n, d)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == PA_DTYPE_F32 ? launch_tiled<float>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st)
+                                       : launch_tiled<pa::f16>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st);
+  return hip_status(e, name);
+}
+
+int pa_fused_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int out_dtype, int64_t bh, int64_t n,
+                 int64_t d, int causal, void* stream) {
+  const char* name = "fused_forward";
+  if (int rc = check_common(name, q, k, v, o, bh, n, d)) return rc;
+  if (d != 64) return fail(PA_ERR_UNSUPPORTED, "%s: only head dimension 64 is compiled (got %lld)", name, (long long)d);
+  if (int rc = check_aligned16(name, q, k, v, o)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (dtype == PA_DTYPE_F32 && out_dtype == PA_DTYPE_F32)
+    e = launch_f32<float, float>(q, k, v, o, (int)bh, (int)n, causal, st);
+  else if (dtype == PA_DTYPE_F16 && out_dtype == PA_DTYPE_F16)
+    e = launch_f32<pa::f16, pa::f16>(q, k, v, o, (int)bh, (int)n, causal, st);
+  else if (dtype == PA_DTYPE_F16 && out_dtype == PA_DTYPE_F32)
+    e = launch_f32<pa::f16, float>(q, k, v, o, (int)bh, (int)n, causal, st);
+  else
+    return fail(PA_ERR_UNSUPPORTED, "%s: only float32 and float16 are supported", name);
+  return hip_status(e, name);
+}
+
+int pa_fused_tuned_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int out_dtype, int64_t bh,
+                       int64_t n, int64_t d, int causal, int double_buffer, int br, int bc, void* stream) {
+  const char* name = "fused_tuned";
+  if (int rc = check_common(name, q, k, v, o, bh, n, d)) return rc;
+  if (dtype != PA_DTYPE_F16) return fail(PA_ERR_UNSUPPORTED, "%s: float16 only", name);
+  if (d != 64) return fail(PA_ERR_UNSUPPORTED, "%s: only head dimension 64 is compiled (got %lld)", name, (long long)d);
+  if (int rc = check_aligned16(name, q, k, v, o)) return rc;
+  const MfmaEntry* e = find_tuned(dtype, out_dtype, d, br, bc, double_buffer);
+  if (!e)
+    return fail(PA_ERR_UNSUPPORTED,
+                "%s: (br, bc) = (%d, %d) not compiled; available: (64,32) (64,64) (128,32) (128,64)", name, br, bc);
+  return hip_status(e->fn(q, k, v, o, (int)bh, (int)n, causal, static_cast<hipStream_t>(stream)), name);
+}
+
+int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int out_dtype, int64_t bh,
+                    int64_t n, int64_t d, int causal, void* stream) {
+  const char* name = "fused_tc";
+  if (int rc = check_common(name, q, k, v, o, bh, n, d)) return rc;
+  if (dtype != PA_DTYPE_F16 && dtype != PA_DTYPE_BF16) return fail(PA_ERR_UNSUPPORTED, "%s: float16 or bfloat16 only", name);
+  if (d != 64 && d != 128)
+    return fail(PA_ERR_UNSUPPORTED, "%s: only head dimensions 64 and 128 are compiled (got %lld)", name, (long long)d);
+  if (int rc = check_aligned16(name, q, k, v, o)) return rc;
+  const MfmaEntry* e = find_tc(dtype, out_dtype, d);
+  if (!e) return fail(PA_ERR_UNSUPPORTED, "%s: output dtype must be the input dtype or float32", name);
+  return hip_status(e->fn(q, k, v, o, (int)bh, (int)n, causal, static_cast<hipStream_t>(stream)), name);
+}
+
+int64_t pa_fused_tuned_lds_bytes(int br, int bc, int double_buffer, int64_t d, int dtype) {
+  const MfmaEntry* e = find_tuned(dtype, dtype, d, br, bc, double_buffer);
+  return e ? e->lds : -1;
+}
+
+int64_t pa_fused_tc_lds_bytes(int64_t d, int dtype) {
+  const MfmaEntry* e = find_tc(dtype, dtype, d);
+  return e ? e->lds : -1;
+}
+
+int pa_device_lds_limit(int device, int64_t* bytes) {
+  if (!bytes) return fail(PA_ERR_INVALID, "pa_device_lds_limit: null output pointer");
+  if (device < 0 || device >= 64) return fail(PA_ERR_INVALID, "pa_device_lds_limit: bad device %d", device);
+  std::lock_guard<std::mutex> lock(g_lds_mu);
+  if (!g_lds_known[device]) {
+    int v = 0;
+    hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device);
+    if (e != hipSuccess) return hip_status(e, "pa_device_lds_limit");
+    g_lds_limit[device] = v;
+    g_lds_known[device] = true;
+  }
+  *bytes = g_lds_limit[device];
+  return PA_OK;
+}
+
+const char* pa_last_error(void) { return g_err; }
+
+const char* pa_version(void) { return "phantom_attn " PA_VERSION_STRING " (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,151 @@
+"""Attention forward kernels for AMD MI355X (gfx950), behind the reference's cuda_attn API.
+
+    import cuda_attn
+    o = cuda_attn.fused_tc(q, k, v, causal=False)   # q, k, v: (B, H, N, d) tensors on the GPU
+
+Drop-in for the reference package (/root/reference/cuda_attn/__init__.py:40-94): same entry
+points, argument defaults, KERNELS ordering and FP16_ONLY set, same argument checks and error
+messages. Underneath, every entry point calls hand-written HIP kernels in libphantom_attn.so
+through its C ABI (include/phantom_attn.h); there is no CPU or PyTorch fallback.
+
+    naive        3 kernels, fp32 N x N scores in a workspace        any d, fp32/fp16
+    tiled        LDS-tiled scores / P.V, one wave per softmax row     any d, fp32/fp16
+    fused        fused online softmax, fp32 arithmetic (fp32 MFMA)    d=64, fp32/fp16
+    fused_tuned  fp16 MFMA fused kernel at a chosen (br, bc) tile and 1 or 2 LDS stages
+    fused_tc     fp16/bf16 MFMA fused kernel                          d=64 or 128
+
+Extensions over the reference: fused_tc accepts bfloat16 and d=128; the fused entry points take
+`out_dtype=torch.float32` to return fp32 output from fp16/bf16 inputs.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _checks, _native
+
+__version__ = "0.1.0"
+
+_DTYPE_CODE = {torch.float32: _native.DTYPE_F32, torch.float16: _native.DTYPE_F16,
+               torch.bfloat16: _native.DTYPE_BF16}
+
+
+def _stream_ptr(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _lds_limit(t: torch.Tensor) -> int:
+    return _native.device_lds_limit(t.device.index if t.device.index is not None else torch.cuda.current_device())
+
+
+def _bhnd(q: torch.Tensor):
+    b, h, n, d = q.shape
+    return b * h, n, d
+
+
+def _call(fn_name: str, err_name: str, device: torch.device, *args) -> None:
+    lib = _native.lib()
+    with torch.cuda.device(device):
+        rc = getattr(lib, fn_name)(*args)
+    _native.check(rc, err_name)
+
+
+def _unfused(fn_name: str, err_name: str, q, k, v, causal: bool) -> torch.Tensor:
+    _checks.check_inputs(q, k, v)
+    _checks.check_float_half(err_name, q)
+    bh, n, d = _bhnd(q)
+    s = torch.empty((q.shape[0], q.shape[1], n, n), dtype=torch.float32, device=q.device)
+    o = torch.empty_like(q)
+    _call(fn_name, err_name, q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), s.data_ptr(),
+          _DTYPE_CODE[q.dtype], bh, n, d, int(bool(causal)), _stream_ptr(q))
+    return o
+
+
+def naive(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False) -> torch.Tensor:
+    """v1: three kernels, one thread per output, N x N scores in HBM."""
+    return _unfused("pa_naive_fwd", "naive_forward", q, k, v, causal)
+
+
+def tiled(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False) -> torch.Tensor:
+    """v2: LDS-tiled matmuls and a wave-per-row softmax, N x N scores still in HBM."""
+    return _unfused("pa_tiled_fwd", "tiled_forward", q, k, v, causal)
+
+
+def fused(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False, *,
+          out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """v3: one fused kernel with online softmax in fp32 arithmetic. Requires d == 64."""
+    _checks.check_inputs(q, k, v)
+    _checks.check_head_dim("fused_forward", q, (64,))
+    _checks.check_float_half("fused_forward", q)
+    od = _checks.resolve_out_dtype("fused_forward", q, out_dtype)
+    bh, n, d = _bhnd(q)
+    o = torch.empty(q.shape, dtype=od, device=q.device)
+    _call("pa_fused_fwd", "fused_forward", q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+          _DTYPE_CODE[q.dtype], _DTYPE_CODE[od], bh, n, d, int(bool(causal)), _stream_ptr(q))
+    return o
+
+
+def fused_tuned(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
+                double_buffer: bool = True, br: int = 64, bc: int = 32, *,
+                out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The fp16 MFMA fused kernel at query tile br and key tile bc.
+    double_buffer=True: two LDS stages, tile t+1 loaded while tile t is computed (v3.2);
+    double_buffer=False: one stage (v3.1). (br, bc) in {(64, 32), (64, 64), (128, 32), (128, 64)}.
+    FP16, d == 64."""
+    _checks.check_inputs(q, k, v)
+    _checks.check_fp16_d64_aligned("fused_tuned", q, k, v)
+    _checks.check_tuned_config(br, bc)
+    od = _checks.resolve_out_dtype("fused_tuned", q, out_dtype)
+    lib = _native.lib()
+    need = lib.pa_fused_tuned_lds_bytes(int(br), int(bc), int(bool(double_buffer)), 64, _native.DTYPE_F16)
+    _checks.check_lds("fused_tuned", need, _lds_limit(q), f"BR={br} BC={bc}")
+    bh, n, d = _bhnd(q)
+    o = torch.empty(q.shape, dtype=od, device=q.device)
+    _call("pa_fused_tuned_fwd", "fused_tuned", q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+          _native.DTYPE_F16, _DTYPE_CODE[od], bh, n, d, int(bool(causal)), int(bool(double_buffer)), int(br), int(bc),
+          _stream_ptr(q))
+    return o
+
+
+def fused_vec(q, k, v, causal=False):
+    """v3.1 with default tiles (one LDS stage)."""
+    return fused_tuned(q, k, v, causal, double_buffer=False)
+
+
+def fused_db(q, k, v, causal=False):
+    """v3.2 with default tiles (two LDS stages)."""
+    return fused_tuned(q, k, v, causal, double_buffer=True)
+
+
+def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False, *,
+             out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """v4: both matmuls on MFMA (fp16/bf16 in, fp32 accumulate), online softmax in between.
+    FP16 or BF16, d in {64, 128}."""
+    _checks.check_inputs(q, k, v)
+    _checks.check_tc(q, k, v)
+    od = _checks.resolve_out_dtype("fused_tc", q, out_dtype)
+    lib = _native.lib()
+    _checks.check_lds("fused_tc", lib.pa_fused_tc_lds_bytes(q.shape[3], _DTYPE_CODE[q.dtype]), _lds_limit(q))
+    bh, n, d = _bhnd(q)
+    o = torch.empty(q.shape, dtype=od, device=q.device)
+    _call("pa_fused_tc_fwd", "fused_tc", q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+          _DTYPE_CODE[q.dtype], _DTYPE_CODE[od], bh, n, d, int(bool(causal)), _stream_ptr(q))
+    return o
+
+
+def reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False) -> torch.Tensor:
+    """FP32 math-backend SDPA (/root/reference/cuda_attn/__init__.py:78-84)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    with sdpa_kernel(SDPBackend.MATH):
+        return torch.nn.functional.scaled_dot_product_attention(
+            q.float(), k.float(), v.float(), is_causal=causal)
+
+
+# Every version, in the order the project builds them.
+KERNELS = {"naive": naive, "tiled": tiled, "fused": fused,
+           "fused_vec": fused_vec, "fused_db": fused_db, "fused_tc": fused_tc}
+# Versions that do not take float32 inputs (fused_tc also takes bfloat16).
+FP16_ONLY = {"fused_vec", "fused_db", "fused_tc"}
+
+__all__ = ["naive", "tiled", "fused", "fused_tuned", "fused_vec", "fused_db", "fused_tc",
+           "reference", "KERNELS", "FP16_ONLY"]
