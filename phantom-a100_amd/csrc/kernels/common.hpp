@@ -46,18 +46,19 @@ __device__ __forceinline__ f32x16 mfma32x32x2(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-// All-reduce across the two 32-lane halves of the wave: lane l and lane l^32 both get
-// op(x[l], x[l^32]). v_permlane32_swap(x, x) hands every lane {x[l%32], x[l%32 + 32]}.
-__device__ __forceinline__ float half_max(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
-                                            false, false);
-  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+// x[l ^ 32]: the value held by the same column in the other half of the wave.
+// v_permlane32_swap(vdst = x, vsrc = x) leaves vdst = {x[l%32]} and vsrc = {x[l%32 + 32]} in every
+// lane, so the partner is vsrc in the low half and vdst in the high half. The two results are
+// selected by lane half on purpose: combining them symmetrically (r0 + r1) is compiled by this
+// hipcc as r0 + r0, which drops the other half.
+__device__ __forceinline__ float partner32(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
 }
-__device__ __forceinline__ float half_sum(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
-                                            false, false);
-  return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-}
+// All-reduce across the two 32-lane halves: lanes l and l^32 both get op(x[l], x[l^32]).
+__device__ __forceinline__ float half_max(float x) { return fmaxf(x, partner32(x)); }
+__device__ __forceinline__ float half_sum(float x) { return x + partner32(x); }
 
 // 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -212,7 +212,11 @@ def test_fused_tc_matches_rounded_p_model(path):
     out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32).cpu().numpy()
     model = oracle.attention_online(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
                                     causal, br=128, bc=64, p_dtype=dt)
-    tol = 2.5e-4 if dt == "float16" else 2e-3
+    # Summation order differs (MFMA vs BLAS), so a P value close to a rounding boundary can round
+    # to the neighbouring fp16/bf16 value; one such flip moves O by at most ulp(p <= 1) * max|V| / l
+    # with l >= 1. Peaked rows (one dominant key) expose single flips; long flat rows average them.
+    ulp1 = 2.0 ** -10 if dt == "float16" else 2.0 ** -7
+    tol = max(2.5e-4, ulp1 * v.float().abs().max().item())
     assert np.abs(out - model).max() <= tol
 
 
