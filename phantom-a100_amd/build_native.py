@@ -68,8 +68,22 @@ def build(verbose: bool = False) -> str:
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     subprocess.run(cmd, check=True)
+    check_no_missing_stubs(tmp)
     os.replace(tmp, OUT)
     return OUT
+
+
+def check_no_missing_stubs(path: str) -> None:
+    """Fail the build if a kernel's host-side launch stub was not emitted (the library would
+    then fail to load with an undefined __device_stub__ symbol)."""
+    nm = shutil.which("nm")
+    if not nm:
+        return
+    out = subprocess.run([nm, "-D", "--undefined-only", path], capture_output=True, text=True, check=True).stdout
+    missing = [ln.split()[-1] for ln in out.splitlines() if "__device_stub__" in ln]
+    if missing:
+        os.remove(path)
+        raise RuntimeError("kernel launch stubs missing from the host object:\n  " + "\n  ".join(missing[:10]))
 
 
 if __name__ == "__main__":

@@ -60,6 +60,28 @@ __device__ __forceinline__ float partner32(float x) {
 __device__ __forceinline__ float half_max(float x) { return fmaxf(x, partner32(x)); }
 __device__ __forceinline__ float half_sum(float x) { return x + partner32(x); }
 
+// Buffer resource over [base, base + bytes): raw buffer loads at offsets past `bytes` return 0
+// without touching memory, which makes the tails of K/V/Q tiles branch-free.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 load16(rsrc_t r, uint32_t byte_offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0);
+}
+
+// 16 bytes per lane from the buffer straight into LDS: lane i writes lds_base + 16*i
+// (lds_base must be wave-uniform); offsets past the buffer's size write zeros.
+__device__ __forceinline__ void load16_to_lds(rsrc_t r, void* lds_base, uint32_t voffset, uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voffset,
+                                           soffset, 0, 0);
+}
+
+// Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002;
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
 // 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -14,16 +14,27 @@
 //        O^T (d x queries)   += V^T . P^T      A = V^T read from LDS with ds_read_b64_tr_b16,
 //                                              B = P^T taken straight from the S^T accumulator
 //    In the 32x32 accumulator, lane l holds column l%32 (= one query) and 16 of its 32 rows
-//    (keys, or head dims), the other 16 sit in lane l^32. So a row max / row sum is a
-//    16-element in-lane reduction plus one v_permlane32_swap, the rescale of O by alpha is
-//    lane-local, and P^T needs no LDS round trip: register r of the S^T block holds key
+//    (keys, or head dims); the other 16 sit in lane l^32. So a row max / row sum is a
+//    16-element in-lane reduction plus one v_permlane32_swap, the rescale of O is lane-local,
+//    and P^T needs no LDS round trip: register r of the S^T block holds key
 //    8*(r/4) + 4*(l/32) + r%4, exactly the key that the PV MFMA's B operand expects in k-slot
-//    8*(l/32) + (r%8) once the A operand (V^T) is read with the same key order.
-//  * K and V tiles of BN keys are staged row-major in LDS (16-byte coalesced global loads,
-//    16-byte LDS writes). With STAGES == 2 the global loads for tile t+1 are issued before the
-//    MFMAs of tile t and written to the other LDS stage afterwards: one barrier per tile.
-//  * LDS rows are padded so that the K operand reads (ds_read_b128, 8..16 consecutive rows at
-//    one column) and the transposed V reads (4 rows x 32 bytes per 16 lanes) hit distinct banks.
+//    8*(l/32) + (r%8) once the A operand (V^T) is read in the same key order.
+//  * K and V tiles of BN keys go HBM -> LDS with buffer_load ... lds (16 bytes per lane, no
+//    VGPR staging; rows past N arrive as zeros). One such load writes 1 KB of LDS contiguously,
+//    so rows are unpadded and 16-byte chunks are XOR-swizzled per row instead: the K operand
+//    reads (ds_read_b128, 16 consecutive rows at one column) and the transposed V reads
+//    (4 rows x 4 chunks per 32 lanes) each touch all 64 banks once.
+//  * STAGES == 2 (default): software pipeline inside each wave. Iteration t runs
+//        phase A: MFMAs of S(t+1) = K(t+1).Q^T   interleaved with the VALU work that turns
+//                                                 S(t) into P(t) (exp2, row sum, rounding)
+//        phase B: MFMAs of O += V(t)^T.P(t)^T    interleaved with the row max of S(t+1)
+//    The interleave is fixed with scheduling-group barriers on a branch-free fast path (tile
+//    t+1 needs no mask); masked tiles (the N tail, causal diagonal) take a generic path. K and
+//    V have their own two-stage LDS rings (K is consumed one tile ahead of V); the loads of
+//    K(t+2) and V(t+1) fly during iteration t; one barrier per tile.
+//  * O and l are rescaled only in tiles where some row's max grew (alpha = 1 exactly
+//    otherwise), a wave-uniform branch; the arithmetic is the reference's.
+//  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
 #pragma once
 
@@ -33,17 +44,29 @@ namespace pa {
 
 template <int D, int BN, int STAGES>
 struct MfmaLds {
-  static constexpr int LDK = D + 8;    // K row pitch in elements (+16 B)
-  static constexpr int LDV = D + 16;   // V row pitch in elements (+32 B)
-  static constexpr int K_ELEMS = BN * LDK;
-  static constexpr int V_ELEMS = BN * LDV;
-  static constexpr int STAGE_ELEMS = K_ELEMS + V_ELEMS;
-  static constexpr int ELEMS = STAGES * STAGE_ELEMS;
-  static constexpr int BYTES = ELEMS * 2;
+  static constexpr int ROW_BYTES = D * 2;
+  static constexpr int TILE_BYTES = BN * ROW_BYTES;
+  static constexpr int BYTES = STAGES * 2 * TILE_BYTES;   // K stages then V stages
 };
 
+// XOR swizzle of the 16-byte chunk index within a row (CR chunks per row).
+// K: consecutive rows r..r+15 read at one logical chunk land in 16 distinct bank groups.
+// V: rows r..r+3 (r % 4 == 0) x chunks 4q..4q+3 land in 16 distinct bank groups.
+template <int CR> __device__ __forceinline__ int k_swz(int row) { return CR == 16 ? (row & 15) : ((row >> 1) & 7); }
+template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 16 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); }
+
+// Minimum waves per SIMD the register allocator must allow (0: compiler default).
+#ifndef PA_MFMA_MIN_WAVES
+#define PA_MFMA_MIN_WAVES 0
+#endif
+#if PA_MFMA_MIN_WAVES > 0
+#define PA_MFMA_OCCUPANCY __attribute__((amdgpu_waves_per_eu(PA_MFMA_MIN_WAVES)))
+#else
+#define PA_MFMA_OCCUPANCY
+#endif
+
 template <typename T, int D, int BM, int BN, int STAGES, typename OutT>
-__global__ void __launch_bounds__(BM / 32 * kWave)
+__global__ void __launch_bounds__(BM / 32 * kWave) PA_MFMA_OCCUPANCY
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
   typedef typename vec8<T>::type V8;
@@ -54,14 +77,18 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   constexpr int NKB = BN / 32;           // 32-key blocks per tile
   constexpr int NDB = D / 32;            // 32-dim blocks of O^T
   constexpr int PV_STEPS = BN / 16;      // MFMA k-steps over the keys of a tile
-  constexpr int CHUNKS_ROW = D / 8;      // 16-byte chunks per K/V row
-  constexpr int CHUNKS = BN * CHUNKS_ROW;
-  static_assert(BM % 32 == 0 && BN % 32 == 0 && D % 32 == 0, "tile shape");
-  static_assert(CHUNKS % THREADS == 0, "K/V tile must split evenly over the workgroup");
-  constexpr int CPT = CHUNKS / THREADS;  // 16-byte chunks per thread per matrix
+  constexpr int CR = D / 8;              // 16-byte chunks per K/V row
+  constexpr int RB = L::ROW_BYTES;
+  constexpr int QK_MFMAS = NKB * QK_STEPS;
+  constexpr int PV_MFMAS = PV_STEPS * NDB;
+  static_assert(D == 64 || D == 128, "head dim");
+  static_assert(BM % 32 == 0 && BN % 32 == 0, "tile shape");
+  static_assert((BN * CR) % THREADS == 0, "K/V tile must split evenly over the workgroup");
+  constexpr int CPT = BN * CR / THREADS; // 16-byte chunks per thread per matrix per tile
   static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
 
-  __shared__ __attribute__((aligned(16))) T lds[L::ELEMS];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[L::BYTES];
+  // stage s of K at lds + s*TILE_BYTES, stage s of V at lds + (STAGES + s)*TILE_BYTES
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
@@ -77,52 +104,54 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   const int q0w = q0 + wave * 32;
   const int qrow = q0w + lq;
   const size_t base = (size_t)bh * N * D;
-  const T* __restrict__ Qb = Q + base;
-  const T* __restrict__ Kb = K + base;
-  const T* __restrict__ Vb = V + base;
+  const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
+  const rsrc_t q_rs = make_rsrc(Q + base, head_bytes);
+  const rsrc_t k_rs = make_rsrc(K + base, head_bytes);
+  const rsrc_t v_rs = make_rsrc(V + base, head_bytes);
 
-  // ---- Q^T operand: lane holds Q[qrow][16*kk + 8*hi + j], j < 8, for every k-step kk.
+  // ---- Q^T operand: lane holds Q[qrow][16*kk + 8*hi + j], j < 8, for every k-step kk
+  // (rows past N read as zero).
   V8 qf[QK_STEPS];
-  {
-    const bool ok = qrow < N;
 #pragma unroll
-    for (int kk = 0; kk < QK_STEPS; ++kk) {
-      V8 z = {};
-      qf[kk] = ok ? *reinterpret_cast<const V8*>(Qb + (size_t)qrow * D + kk * 16 + hi * 8) : z;
-    }
+  for (int kk = 0; kk < QK_STEPS; ++kk)
+    qf[kk] = __builtin_bit_cast(V8, load16(q_rs, (uint32_t)(qrow * RB + kk * 32 + hi * 16)));
+
+  // ---- Direct HBM -> LDS loads. Load i of this thread fills LDS slot i*THREADS + tid of the
+  // tile (16 bytes each, slots in lane order), i.e. row slot/CR at physical chunk slot%CR, which
+  // holds logical chunk (slot%CR) ^ swz(row). The per-lane source offsets are fixed; the tile
+  // start goes in the scalar offset.
+  uint32_t k_src[CPT], v_src[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int slot = i * THREADS + tid;
+    const int row = slot / CR, pc = slot % CR;
+    k_src[i] = (uint32_t)(row * RB + ((pc ^ k_swz<CR>(row)) * 16));
+    v_src[i] = (uint32_t)(row * RB + ((pc ^ v_swz<CR>(row)) * 16));
   }
-
-  // ---- K/V staging: thread handles chunks tid + i*THREADS (row-major, coalesced).
-  u32x4 kreg[CPT], vreg[CPT];
-  auto gload = [&](int j0) {
+  auto load_tile = [&](rsrc_t rs, const uint32_t (&src)[CPT], int lds_off, int j0) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * THREADS;
-      const int row = c / CHUNKS_ROW, col = (c % CHUNKS_ROW) * 8;
-      const int key = j0 + row;
-      u32x4 z = {0u, 0u, 0u, 0u};
-      const bool ok = key < N;
-      kreg[i] = ok ? *reinterpret_cast<const u32x4*>(Kb + (size_t)key * D + col) : z;
-      vreg[i] = ok ? *reinterpret_cast<const u32x4*>(Vb + (size_t)key * D + col) : z;
-    }
+    for (int i = 0; i < CPT; ++i)
+      load16_to_lds(rs, lds + lds_off + (i * THREADS + wave * kWave) * 16, src[i], (uint32_t)(j0 * RB));
   };
-  auto sstore = [&](int st) {
-    T* ks = lds + st * L::STAGE_ELEMS;
-    T* vs = ks + L::K_ELEMS;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * THREADS;
-      const int row = c / CHUNKS_ROW, col = (c % CHUNKS_ROW) * 8;
-      *reinterpret_cast<u32x4*>(ks + row * L::LDK + col) = kreg[i];
-      *reinterpret_cast<u32x4*>(vs + row * L::LDV + col) = vreg[i];
-    }
-  };
+#define k_stage(s_) ((s_) * L::TILE_BYTES)
+#define v_stage(s_) ((STAGES + (s_)) * L::TILE_BYTES)
 
-  // Per-lane source offsets of the transposed V read. In each 16-lane group g, lane i supplies
-  // row (i / 4) and columns 16*(g%2) + 4*(i%4) .. +3; ds_read_b64_tr_b16 then hands lane i the
-  // element (i % 4) of the rows supplied by lanes 4t + i/4, i.e. V[row0 + t][col0 + i], t < 4.
+  // ---- Operand read addresses (byte offsets inside a stage).
+  // K operand of k-step kk: row 32b + lq, logical chunk 2kk + hi.
+  int k_addr[QK_STEPS];
+#pragma unroll
+  for (int kk = 0; kk < QK_STEPS; ++kk) k_addr[kk] = lq * RB + (((2 * kk + hi) ^ k_swz<CR>(lq)) * 16);
+  // V^T operand (transposed read): in each 16-lane group g, lane i supplies row 4*hi + i/4
+  // (+16*ks, +8 for the second half) and logical dims 32*db + 16*(g%2) + 4*(i%4) .. +3;
+  // ds_read_b64_tr_b16 then hands lane i the element i%4 of the rows supplied by lanes
+  // 4t + i/4, i.e. V[row0 + t][32*db + 16*(g%2) + i], t < 4.
   const int g16 = lane / 16, i16 = lane % 16;
-  const int v_lane_off = (hi * 4 + i16 / 4) * L::LDV + 16 * (g16 % 2) + 4 * (i16 % 4);
+  const int v_row = hi * 4 + i16 / 4;
+  const int v_cl = 2 * (g16 % 2) + (i16 % 4) / 2;   // logical chunk within the 4-chunk dim block
+  int v_addr[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    v_addr[db] = v_row * RB + (((4 * db + v_cl) ^ v_swz<CR>(v_row)) * 16) + 8 * (i16 % 2);
 
   float m_run = -INFINITY;  // running max of the log2-domain scores of row qrow
   float l_run = 0.f;        // running sum over the 16 keys per 32 held by this lane
@@ -133,71 +162,86 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   const int kv_end = causal ? min(N, q0 + BM) : N;
   const int ntiles = (kv_end + BN - 1) / BN;
   const int wave_kv_end = causal ? min(kv_end, q0w + 32) : kv_end;  // keys this wave can see
+  const int wave_tiles = (wave_kv_end + BN - 1) / BN;
+  // Tiles [0, clean_tiles) need no mask for this wave: all keys < N and (causal) all keys at or
+  // before the wave's first query.
+  const int clean_tiles = causal ? min(N / BN, (q0w + 1) / BN) : N / BN;
 
-  auto compute = [&](int st, int j0) {
-    const T* ks = lds + st * L::STAGE_ELEMS;
-    const T* vs = ks + L::K_ELEMS;
-
-    // S^T = K . Q^T for each 32-key block.
-    f32x16 s[NKB];
+  // S^T = K . Q^T for the tile in K stage at byte offset `ks`; the 32-key blocks alternate so
+  // that consecutive MFMAs never depend on each other.
+  auto qk = [&](f32x16 (&s)[NKB], int ks) {
 #pragma unroll
-    for (int b = 0; b < NKB; ++b) {
-      s[b] = f32x16{};
+    for (int b = 0; b < NKB; ++b) s[b] = f32x16{};
 #pragma unroll
-      for (int kk = 0; kk < QK_STEPS; ++kk) {
-        const V8 a = *reinterpret_cast<const V8*>(ks + (b * 32 + lq) * L::LDK + kk * 16 + hi * 8);
+    for (int kk = 0; kk < QK_STEPS; ++kk)
+#pragma unroll
+      for (int b = 0; b < NKB; ++b) {
+        const V8 a = *reinterpret_cast<const V8*>(lds + ks + b * 32 * RB + k_addr[kk]);
         s[b] = mfma32x32x16(a, qf[kk], s[b]);
       }
-    }
+  };
 
-    // Mask keys past N and (causal) keys after the query; only tiles that need it pay.
-    const bool need_mask = (j0 + BN > N) || (causal && j0 + BN - 1 > q0w);
-    if (need_mask) {
+  // Mask keys past N and (causal) keys after the query.
+  auto mask = [&](f32x16 (&s)[NKB], int j0) {
 #pragma unroll
-      for (int b = 0; b < NKB; ++b)
+    for (int b = 0; b < NKB; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = j0 + b * 32 + (r / 4) * 8 + hi * 4 + (r % 4);
-          if (key >= N || (causal && key > qrow)) s[b][r] = -INFINITY;
-        }
-    }
+      for (int r = 0; r < 16; ++r) {
+        const int key = j0 + b * 32 + (r / 4) * 8 + hi * 4 + (r % 4);
+        if (key >= N || (causal && key > qrow)) s[b][r] = -INFINITY;
+      }
+  };
 
-    // Online softmax update of this row's state (log2 domain).
+  // Row max of a masked tile: updates m_run and returns alpha = 2^(m_old - m_new) (0 on the
+  // first tile, 1 exactly where the max did not grow); `rescale` is set, wave-uniform, when any
+  // row of the wave grew.
+  auto update_max = [&](const f32x16 (&s)[NKB], bool& rescale) -> float {
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < NKB; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-    mx = half_max(mx);
-    const float m_new = fmaxf(m_run, mx * scale_log2);
-    const bool dead = (m_new == -INFINITY);  // every key so far masked
-    const float alpha = dead ? 0.f : exp2_fast(m_run - m_new);
-    const float neg_m = dead ? 0.f : -m_new;
+    const float m_new = fmaxf(m_run, half_max(mx) * scale_log2);
+    const bool grew = m_new > m_run;
+    rescale = __builtin_amdgcn_ballot_w64(grew) != 0;
+    const float alpha = grew ? exp2_fast(m_run - m_new) : 1.f;  // m_run = -inf -> 0
     m_run = m_new;
+    return alpha;
+  };
 
-    V8 pf[PV_STEPS];
-    float psum = 0.f;
+  // P = 2^(S*c - m) rounded to T as the PV operand; l += sum of the unrounded P.
+  auto exponentiate = [&](const f32x16 (&s)[NKB], V8 (&pf)[PV_STEPS]) {
+    const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;  // fully masked row: P = 0
+    float psum[NKB];
 #pragma unroll
-    for (int b = 0; b < NKB; ++b)
+    for (int b = 0; b < NKB; ++b) {
+      psum[b] = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = exp2_fast(fmaf(s[b][r], scale_log2, neg_m));
-        psum += p;
+        psum[b] += p;
         pf[b * 2 + r / 8][r % 8] = from_f32<T>(p);
       }
-    l_run = l_run * alpha + psum;
+    }
+#pragma unroll
+    for (int b = 0; b < NKB; ++b) l_run += psum[b];
+  };
 
+  auto rescale_o = [&](float alpha) {
+    l_run *= alpha;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+  };
 
-    // O^T += V^T . P^T
+  // O^T += V^T . P^T for the tile in V stage at byte offset `vs`.
+  auto pv = [&](const V8 (&pf)[PV_STEPS], int vs) {
 #pragma unroll
     for (int ks_ = 0; ks_ < PV_STEPS; ++ks_) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const T* p0 = vs + ks_ * 16 * L::LDV + db * 32 + v_lane_off;
+        const unsigned char* p0 = lds + vs + ks_ * 16 * RB + v_addr[db];
         const i16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)(p0));
-        const i16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)(p0 + 8 * L::LDV));
+        const i16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)(p0 + 8 * RB));
         const i16x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
         o[db] = mfma32x32x16(__builtin_bit_cast(V8, a), pf[ks_], o[db]);
       }
@@ -205,24 +249,98 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   };
 
   if constexpr (STAGES == 2) {
-    gload(0);
-    sstore(0);
+    // Prologue: K(0), V(0), K(1) into LDS; S(0) and its row max.
+    load_tile(k_rs, k_src, k_stage(0), 0);
+    load_tile(v_rs, v_src, v_stage(0), 0);
+    if (ntiles > 1) load_tile(k_rs, k_src, k_stage(1), BN);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int t = 0; t < ntiles; ++t) {
-      const int j0 = t * BN;
-      if (t + 1 < ntiles) gload(j0 + BN);          // in flight while tile t is computed
-      if (j0 < wave_kv_end) compute(t & 1, j0);
-      if (t + 1 < ntiles) sstore((t + 1) & 1);
+
+    // Two score buffers swap roles every iteration (the loop is unrolled by two so the swap
+    // costs no register moves).
+    f32x16 sa[NKB], sb[NKB];
+    bool rescale = false;
+    float alpha = 1.f;
+    if (wave_tiles > 0) {
+      qk(sa, k_stage(0));
+      if (clean_tiles < 1) mask(sa, 0);
+      alpha = update_max(sa, rescale);
+    }
+
+    auto iteration = [&](int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB]) {
+      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1). Both arrive
+      // during this iteration and are waited for before its closing barrier.
+      if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(t & 1), (t + 2) * BN);
+      if (t + 1 < ntiles) load_tile(v_rs, v_src, v_stage((t + 1) & 1), (t + 1) * BN);
+      if (t < wave_tiles) {
+        if (rescale) rescale_o(alpha);
+        const int kn = k_stage((t + 1) & 1);
+        const int vc = v_stage(t & 1);
+        V8 pf[PV_STEPS];
+        if (t + 1 < clean_tiles) {
+          // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/sum/round of S(t).
+          qk(sn, kn);
+          exponentiate(s, pf);
+          // K operand reads run two MFMAs ahead of their use.
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+          for (int i = 0; i < QK_MFMAS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, 7, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          // Phase B: PV(t) MFMAs with the row max of S(t+1).
+          pv(pf, vc);
+          alpha = update_max(sn, rescale);
+          // V operand reads (two per MFMA) run two MFMAs ahead of their use.
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+          for (int i = 0; i < PV_MFMAS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          // Generic path: the next tile is masked or absent.
+          const bool ahead = t + 1 < wave_tiles;
+          exponentiate(s, pf);
+          pv(pf, vc);
+          if (ahead) {
+            qk(sn, kn);
+            mask(sn, (t + 1) * BN);
+            alpha = update_max(sn, rescale);
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
+    };
+
+    for (int t = 0; t < ntiles; t += 2) {
+      iteration(t, sa, sb);
+      if (t + 1 < ntiles) iteration(t + 1, sb, sa);
     }
   } else {
     for (int t = 0; t < ntiles; ++t) {
       const int j0 = t * BN;
-      gload(j0);
       __syncthreads();  // previous tile fully consumed
-      sstore(0);
+      load_tile(k_rs, k_src, k_stage(0), j0);
+      load_tile(v_rs, v_src, v_stage(0), j0);
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (j0 < wave_kv_end) compute(0, j0);
+      if (t < wave_tiles) {
+        f32x16 s[NKB];
+        V8 pf[PV_STEPS];
+        bool rescale;
+        qk(s, k_stage(0));
+        if (t >= clean_tiles) mask(s, j0);
+        const float alpha = update_max(s, rescale);
+        if (rescale) rescale_o(alpha);
+        exponentiate(s, pf);
+        pv(pf, v_stage(0));
+      }
     }
   }
 

@@ -42,6 +42,13 @@ int hip_status(hipError_t e, const char* name) {
 
 size_t dtype_bytes(int dt) { return dt == PA_DTYPE_F32 ? 4 : 2; }
 
+// The fused kernels address one head through a 32-bit buffer offset (N*d elements per head).
+int check_head_bytes(const char* name, int64_t n, int64_t d, int dtype) {
+  if ((uint64_t)n * (uint64_t)d * dtype_bytes(dtype) >= (1ull << 31))
+    return fail(PA_ERR_UNSUPPORTED, "%s: one head (N*d*%zu bytes) must stay below 2 GiB", name, dtype_bytes(dtype));
+  return PA_OK;
+}
+
 // Shared argument checks. Pointers must be non-null and 16-byte aligned (the kernels move
 // 16-byte vectors); sizes must keep every in-kernel 32-bit index in range.
 int check_common(const char* name, const void* q, const void* k, const void* v, const void* o,
@@ -206,6 +213,7 @@ int pa_fused_fwd(const void* q, const void* k, const void* v, void* o, int dtype
   if (int rc = check_common(name, q, k, v, o, bh, n, d)) return rc;
   if (d != 64) return fail(PA_ERR_UNSUPPORTED, "%s: only head dimension 64 is compiled (got %lld)", name, (long long)d);
   if (int rc = check_aligned16(name, q, k, v, o)) return rc;
+  if (int rc = check_head_bytes(name, n, d, dtype)) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == PA_DTYPE_F32 && out_dtype == PA_DTYPE_F32)
@@ -226,6 +234,7 @@ int pa_fused_tuned_fwd(const void* q, const void* k, const void* v, void* o, int
   if (dtype != PA_DTYPE_F16) return fail(PA_ERR_UNSUPPORTED, "%s: float16 only", name);
   if (d != 64) return fail(PA_ERR_UNSUPPORTED, "%s: only head dimension 64 is compiled (got %lld)", name, (long long)d);
   if (int rc = check_aligned16(name, q, k, v, o)) return rc;
+  if (int rc = check_head_bytes(name, n, d, dtype)) return rc;
   const MfmaEntry* e = find_tuned(dtype, out_dtype, d, br, bc, double_buffer);
   if (!e)
     return fail(PA_ERR_UNSUPPORTED,
@@ -241,6 +250,7 @@ int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o, int dt
   if (d != 64 && d != 128)
     return fail(PA_ERR_UNSUPPORTED, "%s: only head dimensions 64 and 128 are compiled (got %lld)", name, (long long)d);
   if (int rc = check_aligned16(name, q, k, v, o)) return rc;
+  if (int rc = check_head_bytes(name, n, d, dtype)) return rc;
   const MfmaEntry* e = find_tc(dtype, out_dtype, d);
   if (!e) return fail(PA_ERR_UNSUPPORTED, "%s: output dtype must be the input dtype or float32", name);
   return hip_status(e->fn(q, k, v, o, (int)bh, (int)n, causal, static_cast<hipStream_t>(stream)), name);
