@@ -80,6 +80,7 @@ __device__ __forceinline__ void load16_to_lds(rsrc_t r, void* lds_base, uint32_t
 // Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedValu = 0x002;
 constexpr int kSchedMfma = 0x008;
+constexpr int kSchedVmemRead = 0x020;
 constexpr int kSchedDsRead = 0x100;
 
 // 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0.

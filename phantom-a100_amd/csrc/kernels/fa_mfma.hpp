@@ -38,6 +38,8 @@
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace pa {
@@ -87,8 +89,16 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   constexpr int CPT = BN * CR / THREADS; // 16-byte chunks per thread per matrix per tile
   static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
 
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[L::BYTES];
-  // stage s of K at lds + s*TILE_BYTES, stage s of V at lds + (STAGES + s)*TILE_BYTES
+  // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
+  // cannot alias the operand reads from another, and does not make those reads wait for it.
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[L::TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[L::TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[STAGES == 2 ? L::TILE_BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[STAGES == 2 ? L::TILE_BYTES : 16];
+  auto k_stage = [&](auto par) -> unsigned char* { if constexpr (decltype(par)::value) return k_lds1; else return k_lds0; };
+  auto v_stage = [&](auto par) -> unsigned char* { if constexpr (decltype(par)::value) return v_lds1; else return v_lds0; };
+  const std::integral_constant<int, 0> even{};
+  const std::integral_constant<int, 1> odd{};
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
@@ -128,13 +138,11 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     k_src[i] = (uint32_t)(row * RB + ((pc ^ k_swz<CR>(row)) * 16));
     v_src[i] = (uint32_t)(row * RB + ((pc ^ v_swz<CR>(row)) * 16));
   }
-  auto load_tile = [&](rsrc_t rs, const uint32_t (&src)[CPT], int lds_off, int j0) {
+  auto load_tile = [&](rsrc_t rs, const uint32_t (&src)[CPT], unsigned char* stage, int j0) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i)
-      load16_to_lds(rs, lds + lds_off + (i * THREADS + wave * kWave) * 16, src[i], (uint32_t)(j0 * RB));
+      load16_to_lds(rs, stage + (i * THREADS + wave * kWave) * 16, src[i], (uint32_t)(j0 * RB));
   };
-#define k_stage(s_) ((s_) * L::TILE_BYTES)
-#define v_stage(s_) ((STAGES + (s_)) * L::TILE_BYTES)
 
   // ---- Operand read addresses (byte offsets inside a stage).
   // K operand of k-step kk: row 32b + lq, logical chunk 2kk + hi.
@@ -167,16 +175,16 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // before the wave's first query.
   const int clean_tiles = causal ? min(N / BN, (q0w + 1) / BN) : N / BN;
 
-  // S^T = K . Q^T for the tile in K stage at byte offset `ks`; the 32-key blocks alternate so
-  // that consecutive MFMAs never depend on each other.
-  auto qk = [&](f32x16 (&s)[NKB], int ks) {
+  // S^T = K . Q^T for the tile in K stage `ks`; the 32-key blocks alternate so that
+  // consecutive MFMAs never depend on each other.
+  auto qk = [&](f32x16 (&s)[NKB], const unsigned char* ks) {
 #pragma unroll
     for (int b = 0; b < NKB; ++b) s[b] = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < QK_STEPS; ++kk)
 #pragma unroll
       for (int b = 0; b < NKB; ++b) {
-        const V8 a = *reinterpret_cast<const V8*>(lds + ks + b * 32 * RB + k_addr[kk]);
+        const V8 a = *reinterpret_cast<const V8*>(ks + b * 32 * RB + k_addr[kk]);
         s[b] = mfma32x32x16(a, qf[kk], s[b]);
       }
   };
@@ -233,13 +241,13 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     for (int db = 0; db < NDB; ++db) o[db] *= alpha;
   };
 
-  // O^T += V^T . P^T for the tile in V stage at byte offset `vs`.
-  auto pv = [&](const V8 (&pf)[PV_STEPS], int vs) {
+  // O^T += V^T . P^T for the tile in V stage `vs`.
+  auto pv = [&](const V8 (&pf)[PV_STEPS], const unsigned char* vs) {
 #pragma unroll
     for (int ks_ = 0; ks_ < PV_STEPS; ++ks_) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const unsigned char* p0 = lds + vs + ks_ * 16 * RB + v_addr[db];
+        const unsigned char* p0 = vs + ks_ * 16 * RB + v_addr[db];
         const i16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)(p0));
         const i16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)(p0 + 8 * RB));
         const i16x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
@@ -250,9 +258,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 
   if constexpr (STAGES == 2) {
     // Prologue: K(0), V(0), K(1) into LDS; S(0) and its row max.
-    load_tile(k_rs, k_src, k_stage(0), 0);
-    load_tile(v_rs, v_src, v_stage(0), 0);
-    if (ntiles > 1) load_tile(k_rs, k_src, k_stage(1), BN);
+    load_tile(k_rs, k_src, k_stage(even), 0);
+    load_tile(v_rs, v_src, v_stage(even), 0);
+    if (ntiles > 1) load_tile(k_rs, k_src, k_stage(odd), BN);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -262,20 +270,25 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     bool rescale = false;
     float alpha = 1.f;
     if (wave_tiles > 0) {
-      qk(sa, k_stage(0));
+      qk(sa, k_stage(even));
       if (clean_tiles < 1) mask(sa, 0);
       alpha = update_max(sa, rescale);
     }
 
-    auto iteration = [&](int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB]) {
-      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1). Both arrive
-      // during this iteration and are waited for before its closing barrier.
-      if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(t & 1), (t + 2) * BN);
-      if (t + 1 < ntiles) load_tile(v_rs, v_src, v_stage((t + 1) & 1), (t + 1) * BN);
+    // `par` is the parity of t as a compile-time constant, so every stage below is a fixed LDS
+    // object: K(t+1) in k_stage(!par), V(t) in v_stage(par).
+    auto iteration = [&](auto par, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB]) {
+      constexpr int P = decltype(par)::value;
+      const std::integral_constant<int, P> cur{};
+      const std::integral_constant<int, 1 - P> nxt{};
+      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1). Issued first so
+      // they have the whole iteration to land; waited for before its closing barrier.
+      if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(cur), (t + 2) * BN);
+      if (t + 1 < ntiles) load_tile(v_rs, v_src, v_stage(nxt), (t + 1) * BN);
       if (t < wave_tiles) {
         if (rescale) rescale_o(alpha);
-        const int kn = k_stage((t + 1) & 1);
-        const int vc = v_stage(t & 1);
+        const unsigned char* kn = k_stage(nxt);
+        const unsigned char* vc = v_stage(cur);
         V8 pf[PV_STEPS];
         if (t + 1 < clean_tiles) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/sum/round of S(t).
@@ -319,27 +332,27 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     };
 
     for (int t = 0; t < ntiles; t += 2) {
-      iteration(t, sa, sb);
-      if (t + 1 < ntiles) iteration(t + 1, sb, sa);
+      iteration(even, t, sa, sb);
+      if (t + 1 < ntiles) iteration(odd, t + 1, sb, sa);
     }
   } else {
     for (int t = 0; t < ntiles; ++t) {
       const int j0 = t * BN;
       __syncthreads();  // previous tile fully consumed
-      load_tile(k_rs, k_src, k_stage(0), j0);
-      load_tile(v_rs, v_src, v_stage(0), j0);
+      load_tile(k_rs, k_src, k_stage(even), j0);
+      load_tile(v_rs, v_src, v_stage(even), j0);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (t < wave_tiles) {
         f32x16 s[NKB];
         V8 pf[PV_STEPS];
         bool rescale;
-        qk(s, k_stage(0));
+        qk(s, k_stage(even));
         if (t >= clean_tiles) mask(s, j0);
         const float alpha = update_max(s, rescale);
         if (rescale) rescale_o(alpha);
         exponentiate(s, pf);
-        pv(pf, v_stage(0));
+        pv(pf, v_stage(even));
       }
     }
   }
