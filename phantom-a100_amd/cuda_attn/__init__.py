@@ -29,12 +29,19 @@ _DTYPE_CODE = {torch.float32: _native.DTYPE_F32, torch.float16: _native.DTYPE_F1
                torch.bfloat16: _native.DTYPE_BF16}
 
 
+_LDS_LIMIT: dict = {}
+
+
 def _stream_ptr(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _lds_limit(t: torch.Tensor) -> int:
-    return _native.device_lds_limit(t.device.index if t.device.index is not None else torch.cuda.current_device())
+    dev = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    lim = _LDS_LIMIT.get(dev)
+    if lim is None:
+        lim = _LDS_LIMIT[dev] = _native.device_lds_limit(dev)
+    return lim
 
 
 def _bhnd(q: torch.Tensor):
@@ -43,9 +50,13 @@ def _bhnd(q: torch.Tensor):
 
 
 def _call(fn_name: str, err_name: str, device: torch.device, *args) -> None:
-    lib = _native.lib()
-    with torch.cuda.device(device):
-        rc = getattr(lib, fn_name)(*args)
+    """Launch on `device` (switching the current device only when it differs)."""
+    fn = getattr(_native.lib(), fn_name)
+    if device.index is None or device.index == torch.cuda.current_device():
+        rc = fn(*args)
+    else:
+        with torch.cuda.device(device):
+            rc = fn(*args)
     _native.check(rc, err_name)
 
 
