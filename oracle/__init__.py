@@ -5,7 +5,8 @@ package, and only as the checker or as the timed CPU baseline. The shipped libra
 (phantom-a100_amd/cuda_attn + its HIP .so) never imports it and has no CPU fallback.
 
 Contents:
-  online_softmax.py  NumPy restatement of /root/reference/cuda_attn/online_softmax_ref.py
+  online_softmax.py  NumPy restatement of /root/reference/cuda_attn/online_softmax_ref.py,
+                     plus a model of the MFMA kernel's own arithmetic (attention_kernel_model)
   attn_ref64.c       float64 brute force restating /root/reference/sim/harness.cu:40-64
 """
 from __future__ import annotations
@@ -16,8 +17,8 @@ import subprocess
 
 import numpy as np
 
-from .online_softmax import (LOG2E, attention_f64_rows, attention_naive, attention_online,  # noqa: F401
-                             round_bf16, round_to)
+from .online_softmax import (LOG2E, attention_f64_rows, attention_kernel_model, attention_naive,  # noqa: F401
+                             attention_online, round_bf16, round_to)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB = None

@@ -16,13 +16,20 @@ It restates, in my own NumPy code, the reference's CPU model of the fused kernel
   ``p_dtype`` extends the reference's ``p_fp16`` flag to bfloat16.
 * ``attention_f64_rows`` - float64 truth computed in row blocks, for shapes whose full
   N x N score matrix would not fit in host memory (same math as attention_naive).
+* ``attention_kernel_model`` - not the reference's algorithm: the arithmetic of this build's
+  MFMA kernel (lazy rescale per 32-row wave, l summed from the rounded P), so the GPU test can
+  compare against the same P roundings. Pinned by reducing to ``attention_online`` when the
+  lazy threshold is 0 and P is not rounded, and by the exactness of O / l (below).
 
 How each function is pinned (tests/test_oracle.py): attention_naive against the
 independent C brute force in oracle/attn_ref64.c and closed forms (N=1 -> V, constant
 K -> mean of V, one-hot V -> P, a hand-computed 2x2 case); attention_online against
 attention_naive for the reference's own test matrix (tests/test_algorithm.py:12-46 of
 the reference), tile-size invariance, and an exact-representability check that pins where
-P is rounded; round_bf16 against torch's bfloat16 cast.
+P is rounded; round_bf16 against torch's bfloat16 cast; attention_kernel_model bitwise against
+attention_online at threshold 0 without rounding, against attention_naive at threshold 8
+(O / l is exact for any reference max), by the P <= 2^threshold bound it keeps, and by
+returning V[j] exactly on rows where one key j dominates (l sums the rounded P).
 """
 from __future__ import annotations
 
@@ -143,4 +150,65 @@ def attention_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool =
             o = o * alpha[..., None] + np.matmul(p_mm, v32[..., j0:j1, :])
             m = m_new
         out[..., i0:i1, :] = o / l[..., None]
+    return out
+
+
+def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False,
+                           p_dtype: str | None = None, bc: int = 64, group: int = 32,
+                           lazy_log2: float = 8.0, stats: dict | None = None) -> np.ndarray:
+    """The fused MFMA kernel's arithmetic, in float32 (a model of this build, not the reference).
+
+    Same log2-domain online softmax as ``attention_online``, with the two changes the kernel
+    makes (both exact in real arithmetic):
+      * lazy rescale: rows are taken ``group`` at a time (one wave). After each key tile of
+        ``bc`` keys, if some row's max exceeds its reference max m by more than
+        ``lazy_log2``, every row whose max grew takes it as its new m and O, l are multiplied
+        by alpha = 2^(m_old - m_new); otherwise m is kept and P = 2^(s - m) may reach
+        2^lazy_log2;
+      * l sums the rounded P (the values multiplied into O).
+    ``stats``, if given, receives the largest P used and the number of rescales.
+    """
+    q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
+    *batch, n, d = q32.shape
+    out = np.empty_like(q32)
+    scale_log2 = np.float32(LOG2E / np.sqrt(d))
+    kt = np.swapaxes(k32, -1, -2)
+    thr = np.float32(lazy_log2)
+    p_max, rescales = 0.0, 0
+    for i0 in range(0, n, group):
+        i1 = min(i0 + group, n)
+        qi = q32[..., i0:i1, :] * scale_log2
+        r = i1 - i0
+        rows = np.arange(i0, i1)
+        m = np.full((*batch, r), -np.inf, np.float32)
+        l = np.zeros((*batch, r), np.float32)
+        o = np.zeros((*batch, r, d), np.float32)
+        kv_end = min(n, i1) if causal else n
+        for j0 in range(0, kv_end, bc):
+            j1 = min(j0 + bc, n)
+            s = np.matmul(qi, kt[..., :, j0:j1])
+            if causal:
+                cols = np.arange(j0, j1)
+                s = np.where(cols[None, :] > rows[:, None], np.float32(-np.inf), s)
+            m_cand = np.maximum(m, s.max(axis=-1))
+            with np.errstate(invalid="ignore"):
+                rescale = np.any(m_cand > m + thr, axis=-1, keepdims=True)
+            upd = rescale & (m_cand > m)
+            rescales += int(rescale.sum())
+            with np.errstate(invalid="ignore"):
+                alpha = np.where(upd, np.exp2(m - m_cand), np.float32(1)).astype(np.float32)
+            m = np.where(upd, m_cand, m)
+            dead = np.isneginf(m)
+            with np.errstate(invalid="ignore"):
+                p = np.where(dead[..., None], np.float32(0),
+                             np.exp2(s - m[..., None])).astype(np.float32)
+            p_mm = round_to(p, p_dtype)
+            if p_mm.size:
+                p_max = max(p_max, float(p_mm.max()))
+            l = l * alpha + p_mm.sum(axis=-1, dtype=np.float32)
+            o = o * alpha[..., None] + np.matmul(p_mm, v32[..., j0:j1, :])
+        out[..., i0:i1, :] = o / l[..., None]
+    if stats is not None:
+        stats["p_max"] = p_max
+        stats["rescales"] = rescales
     return out

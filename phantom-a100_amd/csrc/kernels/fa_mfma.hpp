@@ -3,8 +3,16 @@
 // Computes O = softmax(Q K^T / sqrt(d)) V for one (head, BM-query block) per workgroup without
 // materialising the N x N scores. Same math as the reference's v4 kernel
 // (/root/reference/csrc/kernels/fused_tc.cuh:45-179): scores scaled by log2(e)/sqrt(d) in fp32,
-// running max m and sum l per query row, alpha = 2^(m_old - m_new), P rounded to the input
-// dtype only as the P.V operand while l sums the unrounded fp32 P, output O / l.
+// a reference max m and sum l per query row, alpha = 2^(m_old - m_new), P = 2^(S c - m) rounded
+// to the input dtype as the P.V operand, output O / l. Two deliberate differences, both exact
+// in real arithmetic (O / l does not depend on which m is used, as long as numerator and
+// denominator use the same one):
+//  * l sums the rounded P, the values the P.V MFMAs multiply, so the normalisation is
+//    consistent with the numerator (the reference sums the unrounded P). On a row dominated by
+//    one key the rounding of that key's P then cancels in O / l.
+//  * Lazy rescale: m is raised (and O, l multiplied by alpha) only when some row of the wave
+//    would exceed it by more than 2^8; otherwise the stale m is kept and P <= 2^8. The
+//    reference rescales at every tile.
 //
 // gfx950 design (not a translation of the WMMA kernel):
 //  * Each wave owns 32 query rows. Both products are computed transposed so that every
@@ -32,8 +40,9 @@
 //    t+1 needs no mask); masked tiles (the N tail, causal diagonal) take a generic path. K and
 //    V have their own two-stage LDS rings (K is consumed one tile ahead of V); the loads of
 //    K(t+2) and V(t+1) fly during iteration t; one barrier per tile.
-//  * O and l are rescaled only in tiles where some row's max grew (alpha = 1 exactly
-//    otherwise), a wave-uniform branch; the arithmetic is the reference's.
+//  * O and l are rescaled only in tiles where some row's max outgrew the reference max by
+//    more than 2^8 (a wave-uniform branch, rare after the first tile); on the fast path the
+//    rescale runs inside phase A, whose QK MFMAs do not touch O.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
 #pragma once
@@ -73,6 +82,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
   typedef typename vec8<T>::type V8;
   typedef MfmaLds<D, BN, STAGES> L;
+  constexpr float kLazyLog2 = 8.f;       // P stays below 2^kLazyLog2 between rescales
   constexpr int NW = BM / 32;
   constexpr int THREADS = NW * kWave;
   constexpr int QK_STEPS = D / 16;       // MFMA k-steps over the head dim
@@ -200,9 +210,10 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       }
   };
 
-  // Row max of a masked tile: updates m_run and returns alpha = 2^(m_old - m_new) (0 on the
-  // first tile, 1 exactly where the max did not grow); `rescale` is set, wave-uniform, when any
-  // row of the wave grew.
+  // Row max of a masked tile. `rescale` is set, wave-uniform, when some row's max exceeds its
+  // reference max m_run by more than 2^kLazyLog2; then every row whose max grew takes it as its
+  // new m_run. Returns alpha = 2^(m_old - m_new): 0 on a row's first visible tile, exactly 1
+  // where m_run is kept.
   auto update_max = [&](const f32x16 (&s)[NKB], bool& rescale) -> float {
     float mx = -INFINITY;
 #pragma unroll
@@ -210,29 +221,27 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
     const float m_new = fmaxf(m_run, half_max(mx) * scale_log2);
-    const bool grew = m_new > m_run;
-    rescale = __builtin_amdgcn_ballot_w64(grew) != 0;
-    const float alpha = grew ? exp2_fast(m_run - m_new) : 1.f;  // m_run = -inf -> 0
-    m_run = m_new;
+    rescale = __builtin_amdgcn_ballot_w64(m_new > m_run + kLazyLog2) != 0;
+    const bool upd = rescale && m_new > m_run;
+    const float alpha = upd ? exp2_fast(m_run - m_new) : 1.f;  // m_run = -inf -> 0
+    m_run = upd ? m_new : m_run;
     return alpha;
   };
 
-  // P = 2^(S*c - m) rounded to T as the PV operand; l += sum of the unrounded P.
+  // P = 2^(S*c - m) rounded to T: the PV operand.
   auto exponentiate = [&](const f32x16 (&s)[NKB], V8 (&pf)[PV_STEPS]) {
     const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;  // fully masked row: P = 0
-    float psum[NKB];
 #pragma unroll
-    for (int b = 0; b < NKB; ++b) {
-      psum[b] = 0.f;
+    for (int b = 0; b < NKB; ++b)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2_fast(fmaf(s[b][r], scale_log2, neg_m));
-        psum[b] += p;
-        pf[b * 2 + r / 8][r % 8] = from_f32<T>(p);
-      }
-    }
+      for (int r = 0; r < 16; ++r) pf[b * 2 + r / 8][r % 8] = from_f32<T>(exp2_fast(fmaf(s[b][r], scale_log2, neg_m)));
+  };
+  // l += sum of the rounded P (v_dot2 against (1, 1): exact products, fp32 accumulation).
+  auto row_sum = [&](const V8 (&pf)[PV_STEPS]) {
+    float acc[2] = {0.f, 0.f};
 #pragma unroll
-    for (int b = 0; b < NKB; ++b) l_run += psum[b];
+    for (int ks_ = 0; ks_ < PV_STEPS; ++ks_) acc[ks_ % 2] = sum8(pf[ks_], acc[ks_ % 2]);
+    l_run += acc[0] + acc[1];
   };
 
   auto rescale_o = [&](float alpha) {
@@ -286,25 +295,32 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(cur), (t + 2) * BN);
       if (t + 1 < ntiles) load_tile(v_rs, v_src, v_stage(nxt), (t + 1) * BN);
       if (t < wave_tiles) {
-        if (rescale) rescale_o(alpha);
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
         V8 pf[PV_STEPS];
         if (t + 1 < clean_tiles) {
-          // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/sum/round of S(t).
-          qk(sn, kn);
-          exponentiate(s, pf);
-          // K operand reads run two MFMAs ahead of their use.
-          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+          // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/round of S(t) and,
+          // if m moved, the rescale of O and l. Two copies so the common case carries no muls.
+          auto phase_a = [&](auto with_rescale) {
+            constexpr bool RS = decltype(with_rescale)::value;
+            qk(sn, kn);
+            if constexpr (RS) rescale_o(alpha);
+            exponentiate(s, pf);
+            // K operand reads run two MFMAs ahead of their use.
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
 #pragma unroll
-          for (int i = 0; i < QK_MFMAS; ++i) {
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedValu, 7, 0);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-          // Phase B: PV(t) MFMAs with the row max of S(t+1).
+            for (int i = 0; i < QK_MFMAS; ++i) {
+              __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(kSchedValu, RS ? 9 : 5, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          };
+          if (rescale) phase_a(std::true_type{});
+          else phase_a(std::false_type{});
+          // Phase B: PV(t) MFMAs with the row sum of P(t) and the row max of S(t+1).
           pv(pf, vc);
+          row_sum(pf);
           alpha = update_max(sn, rescale);
           // V operand reads (two per MFMA) run two MFMAs ahead of their use.
           __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
@@ -312,13 +328,15 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           for (int i = 0; i < PV_MFMAS; ++i) {
             __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
             __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
           }
           __builtin_amdgcn_sched_barrier(0);
         } else {
           // Generic path: the next tile is masked or absent.
           const bool ahead = t + 1 < wave_tiles;
+          if (rescale) rescale_o(alpha);
           exponentiate(s, pf);
+          row_sum(pf);
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
@@ -352,6 +370,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         const float alpha = update_max(s, rescale);
         if (rescale) rescale_o(alpha);
         exponentiate(s, pf);
+        row_sum(pf);
         pv(pf, v_stage(even));
       }
     }

@@ -204,14 +204,15 @@ def test_golden(path):
 @pytest.mark.parametrize("path", [p for p in GOLDEN if "f16" in os.path.basename(p) or "bf16" in os.path.basename(p)],
                          ids=lambda p: os.path.basename(p)[:-4])
 def test_fused_tc_matches_rounded_p_model(path):
-    """Against the oracle model that rounds P the same way, the MFMA kernel agrees far inside
-    the gate (differences: summation order, and P values that round differently)."""
+    """Against the oracle's model of the kernel's arithmetic (64-key tiles, lazy rescale per
+    32-row wave, P rounded to the input dtype, l from the rounded P), the MFMA kernel agrees far
+    inside the gate (differences: summation order, and P values that round differently)."""
     q, k, v, o, causal, dt, z = load_golden(path)
     if q.shape[-1] not in (64, 128):
         pytest.skip("head dim not compiled for fused_tc")
     out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32).cpu().numpy()
-    model = oracle.attention_online(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
-                                    causal, br=128, bc=64, p_dtype=dt)
+    model = oracle.attention_kernel_model(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                          v.float().cpu().numpy(), causal, p_dtype=dt, bc=64, group=32)
     # Summation order differs (MFMA vs BLAS), so a P value close to a rounding boundary can round
     # to the neighbouring fp16/bf16 value; one such flip moves O by at most ulp(p <= 1) * max|V| / l
     # with l >= 1. Peaked rows (one dominant key) expose single flips; long flat rows average them.

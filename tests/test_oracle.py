@@ -231,3 +231,75 @@ def test_round_bf16_matches_torch():
     want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     got = round_bf16(x)
     assert np.array_equal(np.nan_to_num(want), np.nan_to_num(got))
+
+
+# ---------------------------------------------------------------- 7. model of the MFMA kernel's arithmetic
+@pytest.mark.parametrize("causal", [False, True])
+def test_kernel_model_reduces_to_online_softmax(causal):
+    """Threshold 0 (rescale whenever a max grows) and unrounded P: the same float32 operations
+    as attention_online with 32-row blocks, so the results agree bit for bit."""
+    rng = np.random.default_rng(21)
+    q, k, v = (rng.standard_normal((2, 3, 150, 32)).astype(np.float32) for _ in range(3))
+    got = oracle.attention_kernel_model(q, k, v, causal, p_dtype=None, bc=64, group=32, lazy_log2=0.0)
+    want = attention_online(q, k, v, causal, br=32, bc=64)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [1.0, 4.0])
+def test_kernel_model_lazy_rescale_is_exact(causal, scale):
+    """O / l does not depend on which reference max is used: at threshold 8 (P up to 256) the
+    result still matches float64 softmax to float32 accuracy, and rescales became rare."""
+    rng = np.random.default_rng(22)
+    q, k, v = (rng.standard_normal((1, 2, 300, 64)).astype(np.float32) for _ in range(3))
+    q *= scale
+    st_lazy, st_eager = {}, {}
+    got = oracle.attention_kernel_model(q, k, v, causal, lazy_log2=8.0, stats=st_lazy)
+    oracle.attention_kernel_model(q, k, v, causal, lazy_log2=0.0, stats=st_eager)
+    want = attention_naive(q, k, v, causal)
+    assert np.abs(got - want).max() < 2e-5
+    assert 1.0 <= st_lazy["p_max"] <= 2.0 ** 8
+    assert st_lazy["rescales"] < st_eager["rescales"]
+
+
+def test_kernel_model_keeps_p_below_the_threshold():
+    """Scores that keep growing along the row force rescales; P never exceeds 2^threshold."""
+    n, d = 512, 16
+    q = np.ones((1, 1, n, d), np.float32)
+    k = (np.linspace(0, 12, n, dtype=np.float32)[:, None] * np.ones((1, d), np.float32))[None, None]
+    v = np.random.default_rng(23).standard_normal((1, 1, n, d)).astype(np.float32)
+    for thr in (2.0, 8.0):
+        st = {}
+        got = oracle.attention_kernel_model(q, k, v, lazy_log2=thr, stats=st)
+        assert st["p_max"] <= 2.0 ** thr
+        assert st["rescales"] > 1
+        assert np.abs(got - attention_naive(q, k, v)).max() < 2e-5
+
+
+@pytest.mark.parametrize("p_dtype", ["float16", "bfloat16"])
+def test_kernel_model_dominant_key_returns_its_value(p_dtype):
+    """One key dominates each row (every other P underflows to 0) and the stale max leaves its
+    P = 2^x with fractional x, not representable in p_dtype. Summing l from the rounded P
+    returns that key's V exactly; summing the unrounded P (the reference's rule) would scale it
+    by round(p) / p."""
+    n, d = 64, 64
+    rng = np.random.default_rng(24)
+    v = rng.standard_normal((1, 1, n, d)).astype(np.float32)
+    # tile 0: every row's max is 0 (key 0); tile 1 (keys 32..63, bc=32): key 40 scores
+    # 7.3 (log2 domain) above, inside the lazy threshold, and dominates everything else.
+    s_log2 = np.full((n, n), -200.0, np.float32)
+    s_log2[:, 0] = 0.0
+    s_log2[:, 40] = 7.3
+    d_q = d
+    scale_log2 = np.float32(oracle.LOG2E / np.sqrt(d_q))
+    # realise the scores with q = e_i-style rows: q k^T * scale_log2 = s_log2
+    q = np.eye(n, d_q, dtype=np.float32)[None, None]
+    k = np.zeros((1, 1, n, d_q), np.float32)
+    k[0, 0, :, :n] = (s_log2 / scale_log2).T
+    got = oracle.attention_kernel_model(q, k, v, p_dtype=p_dtype, bc=32, lazy_log2=8.0)
+    p40 = np.float32(2.0) ** np.float32(7.3)
+    w40 = oracle.round_to(np.array([p40], np.float32), p_dtype)[0]
+    want = (w40 * v[0, 0, 40] + v[0, 0, 0]) / (w40 + 1)       # keys 0 and 40 carry all mass
+    np.testing.assert_allclose(got[0, 0], np.broadcast_to(want, (n, d)), rtol=2e-6, atol=2e-6)
+    unrounded_l = (w40 * v[0, 0, 40] + v[0, 0, 0]) / (p40 + 1)
+    assert np.abs(unrounded_l - want).max() > 1e-4
