@@ -1,0 +1,228 @@
+"""Benchmark sweep of the cuda_attn entry points (and torch SDPA) on one MI355X -> CSV.
+
+    python phantom-a100_amd/bench/benchmark.py                         # full sweep
+    python phantom-a100_amd/bench/benchmark.py --ns 1024 4096 --impls fused_tc sdpa_default
+
+Same harness behaviour and CSV schema as the reference's bench/benchmark.py:106-190:
+  * every run is first checked against the fp32 SDPA reference (``cuda_attn.reference``); a
+    result outside the gate is written as ``wrong_result`` and never timed;
+  * timing: warm-up calls, then per timed call a zeroing of a flush buffer followed by one call
+    between two HIP events; median and 10th / 90th percentiles;
+  * peak device memory of one call (torch caching-allocator statistics);
+  * configurations that cannot run are status rows, not crashes: ``unavailable`` (flash-attn is
+    not installed on ROCm here), ``fp16_only``, ``unsupported_d``, ``skipped_oom`` (the N x N
+    score workspace of naive / tiled / sdpa_math would not fit), ``oom``, ``error``.
+MI355X-specific: the flush buffer must exceed the 256 MB Infinity Cache as well as L2, so it is
+max(1 GiB, 2 x L2); ``cc`` records the gfx target and ``cuda`` the HIP version; fused_tc also
+takes bf16 (the reference only fp16), so ``--dtype bf16`` exists.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import os
+import statistics
+import sys
+from datetime import datetime, timezone
+
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), ".."))
+import cuda_attn  # noqa: E402
+from cuda_attn.workloads import attention_flops  # noqa: E402
+
+FIELDS = ["gpu", "cc", "torch", "cuda", "timestamp", "impl", "dtype", "causal", "B", "H", "N", "d",
+          "median_ms", "p10_ms", "p90_ms", "tflops", "peak_mem_mb", "max_abs_err", "status"]
+DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+FLUSH_BYTES_MIN = 1 << 30   # > 256 MB Infinity Cache + L2 on MI355X
+
+
+def sdpa_math(q, k, v, causal):
+    with sdpa_kernel(SDPBackend.MATH):
+        return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+
+def sdpa_default(q, k, v, causal):
+    return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+
+IMPLS = {
+    "naive": cuda_attn.naive,
+    "tiled": cuda_attn.tiled,
+    "fused": cuda_attn.fused,
+    "fused_vec": cuda_attn.fused_vec,
+    "fused_db": cuda_attn.fused_db,
+    "fused_tc": cuda_attn.fused_tc,
+    "sdpa_math": sdpa_math,
+    "sdpa_default": sdpa_default,
+    "flash2": None,  # flash-attn's CUDA package; not installable here
+}
+MATERIALIZES_S = {"naive", "tiled", "sdpa_math"}
+FUSED_HEAD_DIMS = {"fused": (64,), "fused_vec": (64,), "fused_db": (64,), "fused_tc": (64, 128)}
+ACCEPTS = {"fused_vec": (torch.float16,), "fused_db": (torch.float16,),
+           "fused_tc": (torch.float16, torch.bfloat16),
+           "naive": (torch.float16, torch.float32), "tiled": (torch.float16, torch.float32),
+           "fused": (torch.float16, torch.float32)}
+
+
+def gate_tolerance(dtype: torch.dtype) -> float:
+    """The reference's pass bar (/root/reference/bench/benchmark.py:170): 2e-3 for 16-bit inputs."""
+    return 1e-4 if dtype == torch.float32 else 2e-3
+
+
+def workspace_bytes(name: str, b: int, h: int, n: int, d: int, elem: int) -> int:
+    """Device bytes one call allocates: the fp32 N x N scores of the materialising paths (sdpa_math
+    keeps scores and probabilities) plus the output."""
+    out = b * h * n * d * elem
+    if name not in MATERIALIZES_S:
+        return out
+    return b * h * n * n * 4 * (2 if name == "sdpa_math" else 1) + out
+
+
+def fits_in_memory(name: str, b: int, h: int, n: int, d: int, elem: int, free_bytes: int) -> bool:
+    """Skip a materialising kernel whose workspace cannot fit, instead of failing the sweep."""
+    return workspace_bytes(name, b, h, n, d, elem) + 3 * b * h * n * d * elem < 0.85 * free_bytes
+
+
+def status_before_run(name: str, dtype: torch.dtype, d: int) -> str | None:
+    """Status row for a configuration the implementation does not take (None: runnable)."""
+    if IMPLS.get(name) is None:
+        return "unavailable"
+    accepts = ACCEPTS.get(name)
+    if accepts is not None and dtype not in accepts:
+        return "fp16_only" if name in cuda_attn.FP16_ONLY else "unsupported_dtype"
+    if name in FUSED_HEAD_DIMS and d not in FUSED_HEAD_DIMS[name]:
+        return "unsupported_d"
+    return None
+
+
+def time_calls(fn, warmup: int, iters: int, flush_buf: torch.Tensor):
+    """Median, p10, p90 in ms of `iters` calls, each after a cache flush, HIP-event timed on the
+    current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(iters):
+        flush_buf.zero_()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    return summarize(times)
+
+
+def summarize(times: list[float]):
+    times = sorted(times)
+    if len(times) == 1:
+        return times[0], times[0], times[0]
+    q = statistics.quantiles(times, n=10)
+    return statistics.median(times), q[0], q[-1]
+
+
+def peak_memory_mb(fn) -> float:
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    fn()
+    torch.cuda.synchronize()
+    return (torch.cuda.max_memory_allocated() - base) / 2**20
+
+
+def device_meta() -> dict:
+    props = torch.cuda.get_device_properties(0)
+    return dict(gpu=torch.cuda.get_device_name(), cc=getattr(props, "gcnArchName", "").split(":")[0],
+                torch=torch.__version__, cuda=torch.version.hip or "",
+                timestamp=datetime.now(timezone.utc).isoformat(timespec="seconds"))
+
+
+def run_point(name, q, k, v, causal, ref, args, flush_buf, row) -> dict:
+    """One (impl, shape) measurement -> completed CSV row."""
+    b, h, n, d = q.shape
+    st = status_before_run(name, q.dtype, d)
+    if st:
+        return dict(row, status=st)
+    free, _ = torch.cuda.mem_get_info()
+    if not fits_in_memory(name, b, h, n, d, q.element_size(), free):
+        return dict(row, status="skipped_oom")
+    fn_raw = IMPLS[name]
+    fn = lambda: fn_raw(q, k, v, causal)  # noqa: E731
+    try:
+        err = (fn().float() - ref).abs().max().item() if ref is not None else float("nan")
+        if err > gate_tolerance(q.dtype):
+            return dict(row, max_abs_err=f"{err:.2e}", status="wrong_result")
+        iters = args.iters if name != "naive" or n <= 2048 else max(10, args.iters // 10)
+        med, p10, p90 = time_calls(fn, args.warmup, iters, flush_buf)
+        mem = peak_memory_mb(fn)
+    except torch.cuda.OutOfMemoryError:
+        torch.cuda.empty_cache()
+        return dict(row, status="oom")
+    except RuntimeError as e:
+        print(f"{name} N={n}: {e}", file=sys.stderr)
+        return dict(row, status="error")
+    tflops = attention_flops(b, h, n, d, causal) / (med * 1e-3) / 1e12
+    return dict(row, median_ms=f"{med:.4f}", p10_ms=f"{p10:.4f}", p90_ms=f"{p90:.4f}", tflops=f"{tflops:.3f}",
+                peak_mem_mb=f"{mem:.1f}", max_abs_err=f"{err:.2e}", status="ok")
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--impls", nargs="+", default=list(IMPLS), choices=list(IMPLS))
+    p.add_argument("--ns", nargs="+", type=int, default=[512, 1024, 2048, 4096, 8192])
+    p.add_argument("--batch", type=int, default=4)
+    p.add_argument("--heads", type=int, default=16)
+    p.add_argument("--dim", type=int, default=64)
+    p.add_argument("--dtype", choices=list(DTYPES), default="fp16")
+    p.add_argument("--causal", choices=["off", "on", "both"], default="both")
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--iters", type=int, default=100)
+    p.add_argument("--ref-max-n", type=int, default=4096, help="largest N checked against the fp32 reference")
+    p.add_argument("--out", default=None)
+    return p.parse_args(argv)
+
+
+def main(argv=None) -> str:
+    args = parse_args(argv)
+    if not torch.cuda.is_available():
+        raise SystemExit("benchmark.py needs a GPU")
+    dtype = DTYPES[args.dtype]
+    meta = device_meta()
+    out = args.out or os.path.join("results", "measured", f"bench_{meta['gpu'].replace(' ', '_')}.csv")
+    os.makedirs(os.path.dirname(out) or ".", exist_ok=True)
+    causal_modes = {"off": [False], "on": [True], "both": [False, True]}[args.causal]
+    l2 = torch.cuda.get_device_properties(0).L2_cache_size
+    flush_buf = torch.empty(max(2 * l2, FLUSH_BYTES_MIN), dtype=torch.uint8, device="cuda")
+    print(f"# {meta}")
+    gen = torch.Generator().manual_seed(0)
+    with open(out, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=FIELDS)
+        w.writeheader()
+        for causal in causal_modes:
+            for n in args.ns:
+                b, h, d = args.batch, args.heads, args.dim
+                q, k, v = (torch.randn(b, h, n, d, generator=gen).to(dtype).cuda() for _ in range(3))
+                ref = cuda_attn.reference(q, k, v, causal) if n <= args.ref_max_n else None
+                for name in args.impls:
+                    row = dict(meta, impl=name, dtype=args.dtype, causal=causal, B=b, H=h, N=n, d=d)
+                    res = run_point(name, q, k, v, causal, ref, args, flush_buf, row)
+                    w.writerow(res)
+                    fh.flush()
+                    if res["status"] == "ok":
+                        print(f"causal={causal!s:5} N={n:5} {name:12} {float(res['median_ms']):9.3f} ms  "
+                              f"{float(res['tflops']):8.2f} TFLOP/s  {float(res['peak_mem_mb']):9.1f} MB  "
+                              f"err={res['max_abs_err']}")
+                    else:
+                        print(f"causal={causal!s:5} N={n:5} {name:12} {res['status']}")
+                del q, k, v, ref
+                torch.cuda.empty_cache()
+    print(f"wrote {out}")
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -8,10 +8,15 @@ hipcc cross-compiles without a GPU. Flags:
                                          no packed fp32 (v_pk_*_f32) instructions in device code
   -mllvm -amdgpu-mfma-vgpr-form=1        MFMA accumulators in ordinary VGPRs, so the softmax can
                                          read S and rescale O without accvgpr copies
+  -Rpass-analysis=kernel-resource-usage  the compiler's per-kernel resource report (VGPRs, AGPRs,
+                                         SGPRs, spills, scratch, LDS, occupancy), saved beside the
+                                         library as kernel_resources.json for the tile-choice tool
 """
 from __future__ import annotations
 
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -21,6 +26,7 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "cuda_attn", "libphantom_attn.so")
+RESOURCES = os.path.join(HERE, "cuda_attn", "kernel_resources.json")
 SOURCES = ["pa_attn.hip"]
 ARCH = "gfx950"
 
@@ -46,18 +52,22 @@ def build(verbose: bool = False) -> str:
     procs = []
     for src in SOURCES:
         obj = os.path.join(HERE, "_build", os.path.splitext(src)[0] + ".o")
-        cmd = [hipcc(), *DEVICE_FLAGS, *COMMON_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
-               os.path.join(CSRC, src), "-o", obj]
+        cmd = [hipcc(), *DEVICE_FLAGS, *COMMON_FLAGS, "-Rpass-analysis=kernel-resource-usage",
+               "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
         objs.append(obj)
     failed = []
+    resources = {}
     for src, p in procs:
         out, _ = p.communicate()
-        # hipcc's host pass does not know the device-only target feature; that warning is noise.
+        resources.update(parse_resource_remarks(out))
+        # hipcc's host pass does not know the device-only target feature; that warning is noise,
+        # and the resource remarks go to kernel_resources.json.
         lines = [ln for ln in out.splitlines() if "unknown target feature" not in ln and ln.strip()
-                 and "packed-fp32-ops" not in ln]
+                 and "packed-fp32-ops" not in ln and "kernel-resource-usage" not in ln
+                 and not re.match(r"^\s*(\d+ \|.*|\|?\s*\^)$", ln) and not ln.startswith("In file included")]
         if p.returncode != 0:
             failed.append(src)
             print("\n".join(lines), file=sys.stderr)
@@ -70,7 +80,29 @@ def build(verbose: bool = False) -> str:
     subprocess.run(cmd, check=True)
     check_no_missing_stubs(tmp)
     os.replace(tmp, OUT)
+    with open(RESOURCES, "w") as fh:
+        json.dump(resources, fh, indent=1, sort_keys=True)
+        fh.write("\n")
     return OUT
+
+
+_REMARK = re.compile(r"remark:\s+(Function Name|[A-Za-z][A-Za-z ]*?(?: \[[^\]]+\])?):\s*(\S+)\s*\[-Rpass-analysis")
+_FIELDS = {"TotalSGPRs": "sgprs", "VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize [bytes/lane]": "scratch_bytes",
+           "Occupancy [waves/SIMD]": "occupancy_waves_per_simd", "SGPRs Spill": "sgpr_spill",
+           "VGPRs Spill": "vgpr_spill", "LDS Size [bytes/block]": "lds_bytes", "Dynamic Stack": "dynamic_stack"}
+
+
+def parse_resource_remarks(text: str) -> dict:
+    """Per-kernel resources from hipcc -Rpass-analysis=kernel-resource-usage output:
+    {mangled name: {vgprs, agprs, sgprs, scratch_bytes, occupancy_waves_per_simd, ...}}."""
+    out, cur = {}, None
+    for m in _REMARK.finditer(text):
+        key, val = m.group(1).strip(), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None and key in _FIELDS:
+            cur[_FIELDS[key]] = (val == "True") if key == "Dynamic Stack" else int(val)
+    return out
 
 
 def check_no_missing_stubs(path: str) -> None:

@@ -1,0 +1,91 @@
+"""GPU runs of the benchmark harness, the tile sweep and the counter-driven tile choice, at small
+sizes: the CSV rows they write, their status rows, and a rocprofv3-profiled candidate whose
+counters come back observable."""
+from __future__ import annotations
+
+import csv
+import importlib.util
+import os
+import shutil
+import sys
+
+import pytest
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(os.path.dirname(HERE), "phantom-a100_amd")
+sys.path.insert(0, PKG)
+sys.path.insert(0, os.path.join(PKG, "bench"))
+
+pytestmark = pytest.mark.gpu
+
+
+def load(name, path):
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def read_rows(path):
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def test_benchmark_writes_status_and_timing_rows(tmp_path):
+    bm = load("pa_benchmark_gpu", os.path.join(PKG, "bench", "benchmark.py"))
+    out = str(tmp_path / "bench.csv")
+    bm.main(["--ns", "64", "200", "--batch", "1", "--heads", "2", "--iters", "3", "--warmup", "1",
+             "--causal", "both", "--impls", "naive", "tiled", "fused", "fused_vec", "fused_db", "fused_tc",
+             "sdpa_math", "flash2", "--out", out])
+    rows = read_rows(out)
+    assert len(rows) == 2 * 2 * 8
+    assert list(rows[0].keys()) == bm.FIELDS
+    by = {(r["impl"], r["N"], r["causal"]): r for r in rows}
+    for impl in ("naive", "tiled", "fused", "fused_vec", "fused_db", "fused_tc", "sdpa_math"):
+        r = by[(impl, "200", "True")]
+        assert r["status"] == "ok", r
+        assert float(r["median_ms"]) > 0 and float(r["tflops"]) > 0 and float(r["max_abs_err"]) <= 2e-3
+    assert by[("flash2", "64", "False")]["status"] == "unavailable"
+    assert rows[0]["cc"].startswith("gfx9")
+
+
+def test_benchmark_bf16_and_unsupported_rows(tmp_path):
+    bm = load("pa_benchmark_gpu2", os.path.join(PKG, "bench", "benchmark.py"))
+    out = str(tmp_path / "bench_bf16.csv")
+    bm.main(["--ns", "128", "--batch", "1", "--heads", "2", "--dim", "128", "--dtype", "bf16", "--iters", "3",
+             "--warmup", "1", "--causal", "off", "--impls", "fused_tc", "fused", "fused_vec", "--out", out])
+    st = {r["impl"]: r["status"] for r in read_rows(out)}
+    assert st == {"fused_tc": "ok", "fused": "unsupported_dtype", "fused_vec": "fp16_only"}
+
+
+def test_sweep_tiles_covers_every_compiled_tile(tmp_path):
+    sw = load("pa_sweep_gpu", os.path.join(PKG, "bench", "sweep_tiles.py"))
+    out = str(tmp_path / "tiles.csv")
+    sw.main(["--ns", "256", "--batch", "1", "--heads", "2", "--iters", "3", "--out", out])
+    rows = read_rows(out)
+    assert len(rows) == 8 and all(r["status"] == "ok" for r in rows)
+    assert {(int(r["br"]), int(r["bc"]), r["double_buffer"]) for r in rows} == \
+        {(br, bc, db) for br, bc in ((64, 32), (64, 64), (128, 32), (128, 64)) for db in ("False", "True")}
+
+
+def test_select_tiles_picks_the_fastest_passing_candidate():
+    from autotune import select_tiles as st
+    best = st.main(["--entry", "fused_tuned", "--n", "512", "--batch", "1", "--heads", "4", "--iters", "3"])
+    assert best is not None and best["status"] == "ok"
+    assert best["regs"] > 0 and 1 <= best["waves_per_simd_limit"] <= 8
+
+
+@pytest.mark.skipif(shutil.which("rocprofv3") is None, reason="rocprofv3 not installed")
+def test_select_tiles_profiles_a_candidate(tmp_path):
+    """fused_tc at a small bf16 d=128 shape under rocprofv3: the counters the rules use come back."""
+    from autotune import select_tiles as st
+    out = str(tmp_path / "report.md")
+    best = st.main(["--entry", "fused_tc", "--dtype", "bf16", "--dim", "128", "--n", "1024", "--batch", "1",
+                    "--heads", "8", "--iters", "3", "--profile", "--profile-dir", str(tmp_path / "prof"),
+                    "--pass-timeout", "90", "--out", out])
+    assert best is not None and best.get("profile_status") == "ok", best
+    for key in ("mfma_util", "valu_busy", "hbm_bytes", "occupancy", "lds_active_cycles", "wait_frac"):
+        assert best.get(key) is not None, key
+    assert 0 < best["mfma_util"] <= 100
+    assert os.path.exists(out) and "Chosen" in open(out).read()

@@ -1,0 +1,235 @@
+"""CPU tests of the benchmark harness (phantom-a100_amd/bench) and the counter-driven tile choice
+(phantom-a100_amd/autotune): status rules, the CSV schema, counter-pass limits, parsing of
+rocprofv3 and compiler output recorded on gfx950 (tests/golden/rocprof), the occupancy model and
+the bottleneck rules. The GPU runs of the same tools are in test_gpu_tools.py."""
+from __future__ import annotations
+
+import importlib.util
+import os
+import sys
+
+import pytest
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(os.path.dirname(HERE), "phantom-a100_amd")
+FIX = os.path.join(HERE, "golden", "rocprof")
+sys.path.insert(0, PKG)
+
+from autotune import diagnose as dg  # noqa: E402
+from autotune import hw_counters as hc  # noqa: E402
+from autotune import select_tiles as st  # noqa: E402
+
+
+def load(name, path):
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+benchmark = load("pa_benchmark", os.path.join(PKG, "bench", "benchmark.py"))
+build_native = load("pa_build_native", os.path.join(PKG, "build_native.py"))
+
+
+# ---------------------------------------------------------------- benchmark harness
+def test_csv_schema_is_the_references():
+    # /root/reference/bench/benchmark.py:132-133
+    assert benchmark.FIELDS == ["gpu", "cc", "torch", "cuda", "timestamp", "impl", "dtype", "causal", "B", "H", "N",
+                                "d", "median_ms", "p10_ms", "p90_ms", "tflops", "peak_mem_mb", "max_abs_err", "status"]
+
+
+@pytest.mark.parametrize("name,dtype,d,want", [
+    ("flash2", torch.float16, 64, "unavailable"),
+    ("fused_vec", torch.float32, 64, "fp16_only"),
+    ("fused_db", torch.bfloat16, 64, "fp16_only"),
+    ("fused_tc", torch.float32, 64, "fp16_only"),
+    ("fused_tc", torch.bfloat16, 128, None),
+    ("fused_tc", torch.float16, 80, "unsupported_d"),
+    ("fused", torch.float32, 128, "unsupported_d"),
+    ("fused", torch.float32, 64, None),
+    ("naive", torch.bfloat16, 64, "unsupported_dtype"),
+    ("naive", torch.float16, 80, None),
+    ("sdpa_math", torch.bfloat16, 80, None),
+])
+def test_status_rows(name, dtype, d, want):
+    assert benchmark.status_before_run(name, dtype, d) == want
+
+
+def test_workspace_accounting():
+    b, h, n, d = 4, 16, 8192, 64
+    s = b * h * n * n * 4
+    o = b * h * n * d * 2
+    assert benchmark.workspace_bytes("naive", b, h, n, d, 2) == s + o
+    assert benchmark.workspace_bytes("sdpa_math", b, h, n, d, 2) == 2 * s + o
+    assert benchmark.workspace_bytes("fused_tc", b, h, n, d, 2) == o
+    assert not benchmark.fits_in_memory("naive", b, h, n, d, 2, free_bytes=16 << 30)
+    assert benchmark.fits_in_memory("naive", b, h, n, d, 2, free_bytes=288 << 30)
+    assert benchmark.fits_in_memory("fused_tc", b, h, n, d, 2, free_bytes=1 << 30)
+
+
+def test_summary_statistics():
+    med, p10, p90 = benchmark.summarize([float(x) for x in range(1, 101)])
+    assert med == 50.5 and p10 < 12 and p90 > 89
+    assert benchmark.summarize([2.0]) == (2.0, 2.0, 2.0)
+
+
+def test_flush_buffer_exceeds_infinity_cache():
+    assert benchmark.FLUSH_BYTES_MIN > 256 * 2**20
+
+
+# ---------------------------------------------------------------- counter passes and parsing
+def test_passes_fit_the_hardware_limits():
+    for p in hc.PASSES:
+        hc.check_pass(p)
+    with pytest.raises(ValueError):
+        hc.check_pass(["FETCH_SIZE", "WRITE_SIZE"])           # 5 TCC counters
+    with pytest.raises(ValueError):
+        hc.check_pass([f"SQ_X{i}" for i in range(9)])           # 9 SQ counters
+    with pytest.raises(ValueError):
+        hc.check_pass(["GRBM_GUI_ACTIVE", "GRBM_COUNT", "GRBM_X"])
+
+
+def test_every_mapped_counter_is_collected_by_some_pass():
+    collected = {c for p in hc.PASSES for c in p}
+    for key, m in hc.MAPPING.items():
+        for c in m["counters"]:
+            assert c in collected, (key, c)
+
+
+def fixture_passes():
+    return [hc.parse_counter_csv(os.path.join(FIX, f"c4_pass{i}_counter_collection.csv")) for i in range(4)]
+
+
+def test_fixture_passes_are_the_tools_passes():
+    for p, rows in zip(hc.PASSES, fixture_passes()):
+        names = {k for d in rows.values() for k in d if k.isupper()}
+        assert names == set(p)
+
+
+def test_parse_counter_csv_and_aggregate():
+    """C4 (bf16, B=4 H=32 N=4096 d=128) profiled on MI355X by select_tiles.py: one copy of 1 GiB
+    (the FETCH_SIZE calibration) and the steady-state fused_tc dispatch."""
+    passes = fixture_passes()
+    d, calib = hc.merge_passes(passes, "fa_mfma_fwd")
+    assert 1.9 < calib < 2.1                              # FETCH_SIZE reads half of a copy's bytes
+    for c in {c for p in hc.PASSES for c in p} - {"SQ_LDS_BANK_CONFLICT"}:
+        assert d[c] is not None and d[c] > 0, c
+    assert d["SQ_LDS_BANK_CONFLICT"] == 0                 # the XOR-swizzled K/V rows never conflict
+    assert d["grid"] == 1048576 and d["workgroup"] == 512 and d["lds"] == 65536
+    trace = hc.parse_kernel_trace(os.path.join(FIX, "c4_kernel_trace.csv"))
+    d["duration_ns"] = trace[-1]["duration_ns"]
+    agg = hc.aggregate([d], {"vgprs": 238, "agprs": 0, "lds_bytes": 65536}, fetch_calibration=calib)
+    compulsory = (3 * 2 + 2) * 128 * 4096 * 128
+    assert abs(agg["hbm_bytes"] / compulsory - 1) < 0.01  # C4 streams Q, K, V, O once
+    assert 30 < agg["mfma_util"] < 80                     # about 52 % in the committed C4 profile
+    assert agg["waves_per_simd_limit"] == 2 and agg["occupancy_limiter"] == "vgpr"
+    assert 10 < agg["occupancy"] <= 25                    # 2 of 8 waves per SIMD resident at most
+    assert 0 < agg["wait_frac"] < 1
+    assert agg["workgroups"] == 2048
+    flops = 4 * 128 * 4096 ** 2 * 128
+    assert 500 < flops / (agg["cycles"] * 1e-9) / 1e12 < 2000   # the trace's kernel time is the C4 rate
+
+
+def test_aggregate_formulas_on_known_numbers():
+    grbm_per_xcd = 1_000_000
+    d = {"kernel": "k", "duration_ns": 1000, "grid": 256 * 64, "workgroup": 64,
+         "GRBM_GUI_ACTIVE": grbm_per_xcd * hc.XCDS,
+         "SQ_VALU_MFMA_BUSY_CYCLES": 0.25 * grbm_per_xcd * hc.CUS * hc.SIMDS_PER_CU,
+         "SQ_WAVE_CYCLES": 0.5 * grbm_per_xcd * hc.CUS * 32 / 4,
+         "SQ_ACTIVE_INST_VALU": 0.4 * grbm_per_xcd * hc.CUS,
+         "SQ_WAIT_INST_ANY": 0.2 * 0.5 * grbm_per_xcd * hc.CUS * 32 / 4,   # 20 % of the wave cycles
+         "FETCH_SIZE": 100.0, "WRITE_SIZE": 50.0}
+    a = hc.aggregate([d], None, fetch_calibration=2.0)
+    assert a["mfma_util"] == pytest.approx(25.0)
+    assert a["occupancy"] == pytest.approx(50.0)
+    assert a["valu_busy"] == pytest.approx(40.0)
+    assert a["wait_frac"] == pytest.approx(0.2)
+    assert a["hbm_bytes"] == pytest.approx(100 * 1024 * 2 + 50 * 1024)
+    missing = hc.aggregate([{"kernel": "k", "duration_ns": 5}], None)
+    assert missing["mfma_util"] is None and missing["hbm_bytes"] is None   # unobservable, not zero
+
+
+def test_parse_kernel_trace():
+    rows = hc.parse_kernel_trace(os.path.join(FIX, "c4_kernel_trace.csv"))
+    assert len(rows) == 4 and "fa_mfma_fwd" in rows[-1]["kernel"]
+    assert all(r["duration_ns"] > 0 for r in rows)
+    assert rows[-1]["grid"] == 1048576 and rows[-1]["workgroup"] == 512
+
+
+# ---------------------------------------------------------------- compiler resources and occupancy
+def resources_fixture():
+    with open(os.path.join(FIX, "resource_remarks.txt")) as fh:
+        return build_native.parse_resource_remarks(fh.read())
+
+
+def test_parse_resource_remarks():
+    res = resources_fixture()
+    assert len(res) == 5
+    c4 = [v for k, v in res.items() if "fa_mfma_fwdIDF16bLi128ELi256ELi64ELi2EDF16b" in k][0]
+    assert c4["vgprs"] == 238 and c4["agprs"] == 0 and c4["lds_bytes"] == 65536
+    assert c4["occupancy_waves_per_simd"] == 2 and c4["vgpr_spill"] == 0 and c4["scratch_bytes"] == 0
+
+
+def test_vgpr_occupancy_model_agrees_with_the_compiler():
+    """Our VGPR limit (512 registers per lane, granule 8, at most 8 waves) gives the compiler's
+    reported occupancy for every kernel of the fixture (none of them is LDS-limited at its launch
+    size)."""
+    for name, r in resources_fixture().items():
+        waves, _ = hc.theoretical_waves_per_simd(r["vgprs"], r["agprs"], 0, 64)
+        assert waves == r["occupancy_waves_per_simd"], name
+
+
+@pytest.mark.parametrize("vgprs,lds,threads,want", [
+    (238, 65536, 512, (2, "vgpr")),
+    (96, 8192, 256, (5, "vgpr")),
+    (128, 16384, 256, (4, "vgpr")),
+    (64, 65536, 256, (2, "lds")),        # 2 workgroups of 4 waves fit in 160 KB
+    (16, 0, 64, (8, "waves")),
+])
+def test_theoretical_waves(vgprs, lds, threads, want):
+    assert hc.theoretical_waves_per_simd(vgprs, 0, lds, threads) == want
+
+
+def test_candidates_name_compiled_kernels():
+    res = resources_fixture()
+    # the fixture holds one fused_tuned instantiation and the d=128 fused_tc one
+    assert st.find_resources(res, st.kernel_key(torch.float16, 64, 128, 32, 1, torch.float16))
+    assert st.find_resources(res, st.kernel_key(torch.bfloat16, 128, 256, 64, 2, torch.bfloat16))
+    assert len(st.candidates("fused_tuned", 64)) == 8
+    assert st.candidates("fused_tc", 128) == [("br256_bc64_2stage", 256, 64, 2)]
+
+
+# ---------------------------------------------------------------- bottleneck rules
+def test_rules_fire_on_their_evidence():
+    comp = 1e6
+    cases = {
+        "materialized_intermediate": dict(kernel_launches=3, hbm_bytes=5e6),
+        "redundant_hbm_traffic": dict(hbm_bytes=3.5e6),
+        "vgpr_limited_occupancy": dict(waves_per_simd_limit=1, occupancy_limiter="vgpr", regs=300),
+        "lds_limited_occupancy": dict(waves_per_simd_limit=1, occupancy_limiter="lds"),
+        "scalar_math_bound": dict(mfma_insn=0, valu_busy=80.0),
+        "valu_bound_softmax": dict(mfma_insn=100, mfma_util=40.0, valu_busy=55.0),
+        "lds_bank_conflicts": dict(lds_bank_conflict_cycles=10.0, lds_active_cycles=100.0),
+        "latency_bound": dict(wait_frac=0.7, occupancy=20.0),
+        "low_parallelism": dict(workgroups=42, resident_wgs_per_cu=2),
+        "register_spills": dict(spill=16),
+    }
+    assert set(cases) == set(dg.THRESHOLDS)
+    for rule, counters in cases.items():
+        got = [b.name for b in dg.diagnose(counters, comp)]
+        assert rule in got, (rule, got)
+        assert all(b.severity >= 1 for b in dg.diagnose(counters, comp))
+
+
+def test_clean_point_triggers_nothing():
+    c4_like = dict(kernel_launches=1, hbm_bytes=1.0004e6, waves_per_simd_limit=2, occupancy_limiter="vgpr",
+                   mfma_insn=1000, mfma_util=65.0, valu_busy=43.0, lds_bank_conflict_cycles=0.0,
+                   lds_active_cycles=100.0, wait_frac=0.3, occupancy=25.0, workgroups=2048,
+                   resident_wgs_per_cu=1, spill=0)
+    assert dg.diagnose(c4_like, 1e6) == []
+
+
+def test_unobservable_inputs_disable_rules():
+    assert dg.diagnose({}, None) == []
+    assert dg.resident_wgs_per_cu(2, 512) == 1 and dg.resident_wgs_per_cu(4, 256) == 4
