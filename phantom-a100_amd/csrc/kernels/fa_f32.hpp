@@ -3,44 +3,81 @@
 // Same algorithm and numerics as the reference's v3 kernel
 // (/root/reference/csrc/kernels/fused.cuh:26-102): Q pre-scaled by log2(e)/sqrt(d) in fp32
 // registers, scores, running max/sum and P all fp32 (P is never rounded), inputs fp32 or fp16
-// widened to fp32 when staged. On gfx950 both products run on the fp32 matrix core
-// (v_mfma_f32_32x32x2_f32) instead of one thread per row on scalar FMAs:
-//   S^T (keys x queries) = K . Q^T   A = K from LDS (ds_read_b128 feeds 4 k-steps),
+// widened to fp32 on load. Both products run on the fp32 matrix core (v_mfma_f32_32x32x2_f32):
+//   S^T (keys x queries) = K . Q^T   A = K (lane: one key row, 32 consecutive dims),
 //                                    B = scaled Q^T in VGPRs, k-slot h of step kk = dim h*D/2+kk
 //   O^T (d x queries)   += V^T . P^T  B = P^T straight from the S^T accumulator (k-slot h of
-//                                    step r = key 8*(r/4) + 4*h + r%4), A = V read row-major
-//                                    from LDS (32 consecutive dims per half-wave, no transpose)
-// Each wave owns 32 query rows; lane l keeps all state of query l%32 (see fa_mfma.hpp).
+//                                    step r = key 8*(r/4) + 4*h + r%4), A = V (lane: one dim of
+//                                    the two keys of the step)
+// Each lane keeps all state of query l%32 (see fa_mfma.hpp).
+//
+// gfx950 shape: the fp32 matrix core does 64 FLOP per cycle per SIMD, so a 32-query x 32-key
+// tile costs a wave ~4K cycles; at the reference's sizes (N = 128) a wave per 32 queries leaves
+// most SIMDs idle and runs four tiles back to back. Here a workgroup of KS waves owns 32 query
+// rows and SPLITS THE KEYS: wave w takes key tiles w, w+KS, w+2KS, ... with its own running
+// (m, l, O); the KS partial states are merged once through LDS at the end with the same rule
+// the online softmax applies between tiles (m = max m_w, l = sum l_w 2^(m_w - m),
+// O = sum O_w 2^(m_w - m)), the reference's merge_ml (tiled.cuh:48-53) extended to O. Each wave
+// reads its K/V rows straight from HBM/L2 into the operand registers (no tile is shared between
+// waves, so no LDS staging), one tile ahead of its use.
 #pragma once
 
 #include "common.hpp"
 
 namespace pa {
 
-template <int D, int BN>
+template <int D, int KS>
 struct F32Lds {
-  static constexpr int LDK = D + 4;   // +16 B: 8/16 consecutive K rows at one column hit distinct banks
-  static constexpr int LDV = D + 8;   // +32 B: the two half-waves read rows 4 apart on distinct banks
-  static constexpr int BYTES = BN * (LDK + LDV) * 4;
+  static constexpr int LDO = D + 4;   // +16 B per query row: the 32 rows written at one column hit distinct banks
+  static constexpr int BYTES = KS * 32 * (LDO + 2) * 4;
 };
 
-template <typename T, int D, int BM, int BN, typename OutT>
-__global__ void __launch_bounds__(BM / 32 * kWave)
+// 32 consecutive elements of a row, widened to fp32 (offsets past the buffer read as zero).
+// The loaded vector is bit-cast as a whole before its elements are taken: bit-casting an element
+// extracted from the u32x4 miscompiles with this toolchain (every element read as element 0).
+template <typename T>
+__device__ __forceinline__ void load_row32(rsrc_t rs, uint32_t byte_off, float (&x)[32]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4 w = __builtin_bit_cast(f32x4, load16(rs, byte_off + 16 * i));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * i + j] = w[j];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 w = load16(rs, byte_off + 16 * i);
+      const f16x8 h = __builtin_bit_cast(f16x8, w);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)h[j];
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float load_one(rsrc_t rs, uint32_t byte_off) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, byte_off, 0, 0));
+  } else {
+    return (float)__builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(rs, byte_off, 0, 0));
+  }
+}
+
+template <typename T, int D, int KS, typename OutT>
+__global__ void __launch_bounds__(KS * kWave)
 fa_f32_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
            OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
-  typedef F32Lds<D, BN> L;
-  constexpr int NW = BM / 32;
-  constexpr int THREADS = NW * kWave;
-  constexpr int NKB = BN / 32;
+  typedef F32Lds<D, KS> L;
+  constexpr int BN = 32;                     // keys per tile
   constexpr int NDB = D / 32;
   constexpr int HALF = D / 2;
-  constexpr int QUADS = BN * D / 4;          // 4-element groups per K/V tile
-  static_assert(D % 32 == 0 && BN % 32 == 0 && BM % 32 == 0, "tile shape");
-  static_assert(QUADS % THREADS == 0, "K/V tile must split evenly over the workgroup");
-  constexpr int QPT = QUADS / THREADS;
+  constexpr int ES = sizeof(T);
+  static_assert(D == 64, "the fp32 path is compiled for d = 64");
 
-  __shared__ __attribute__((aligned(16))) float ks[BN * L::LDK];
-  __shared__ __attribute__((aligned(16))) float vs[BN * L::LDV];
+  __shared__ __attribute__((aligned(16))) float red_o[KS * 32 * L::LDO];
+  __shared__ float red_m[KS * 32];
+  __shared__ float red_l[KS * 32];
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
@@ -52,91 +89,59 @@ fa_f32_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict
   const int bh = blk / num_qblocks;
   int qb = blk % num_qblocks;
   if (causal) qb = num_qblocks - 1 - qb;
-  const int q0 = qb * BM;
-  const int q0w = q0 + wave * 32;
-  const int qrow = q0w + lq;
+  const int q0 = qb * 32;
+  const int qrow = q0 + lq;
   const size_t base = (size_t)bh * N * D;
-  const T* __restrict__ Qb = Q + base;
-  const T* __restrict__ Kb = K + base;
-  const T* __restrict__ Vb = V + base;
+  const uint32_t head_bytes = (uint32_t)((size_t)N * D * ES);
+  const rsrc_t q_rs = make_rsrc(Q + base, head_bytes);
+  const rsrc_t k_rs = make_rsrc(K + base, head_bytes);
+  const rsrc_t v_rs = make_rsrc(V + base, head_bytes);
 
-  // Scaled Q^T operand: k-slot `hi` of step kk is dim hi*HALF + kk.
+  // Scaled Q^T operand: k-slot `hi` of step kk is dim hi*HALF + kk (rows past N read as zero).
   float qf[HALF];
-  {
-    const bool ok = qrow < N;
+  load_row32<T>(q_rs, (uint32_t)((qrow * D + hi * HALF) * ES), qf);
 #pragma unroll
-    for (int c = 0; c < HALF; ++c) qf[c] = ok ? to_f32(Qb[(size_t)qrow * D + hi * HALF + c]) * scale_log2 : 0.f;
-  }
+  for (int c = 0; c < HALF; ++c) qf[c] *= scale_log2;
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
 
-  const int kv_end = causal ? min(N, q0 + BM) : N;
-  const int wave_kv_end = causal ? min(kv_end, q0w + 32) : kv_end;
+  const int kv_end = causal ? min(N, q0 + 32) : N;
+  const int ntiles = (kv_end + BN - 1) / BN;
 
-  for (int j0 = 0; j0 < kv_end; j0 += BN) {
-    // Stage K/V rows [j0, j0 + BN) as fp32 (zeros past N).
-    float4 kq[QPT], vq[QPT];
+  // Operands of one tile: K row (key j0 + lq, dims hi*HALF ..) and V (dim db*32 + lq of the key
+  // that k-slot hi of step r holds).
+  struct Tile {
+    float k[HALF];
+    float v[16][NDB];
+  };
+  auto load_tile = [&](Tile& tl, int j0) {
+    load_row32<T>(k_rs, (uint32_t)(((j0 + lq) * D + hi * HALF) * ES), tl.k);
 #pragma unroll
-    for (int i = 0; i < QPT; ++i) {
-      const int c = tid + i * THREADS;
-      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
-      const int key = j0 + row;
-      float4 kk = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-      if (key < N) {
-        const T* kp = Kb + (size_t)key * D + col;
-        const T* vp = Vb + (size_t)key * D + col;
-        kk = make_float4(to_f32(kp[0]), to_f32(kp[1]), to_f32(kp[2]), to_f32(kp[3]));
-        vv = make_float4(to_f32(vp[0]), to_f32(vp[1]), to_f32(vp[2]), to_f32(vp[3]));
-      }
-      kq[i] = kk;
-      vq[i] = vv;
-    }
-    __syncthreads();  // previous tile fully consumed
+    for (int r = 0; r < 16; ++r) {
+      const int key = j0 + 8 * (r / 4) + 4 * hi + (r % 4);
 #pragma unroll
-    for (int i = 0; i < QPT; ++i) {
-      const int c = tid + i * THREADS;
-      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
-      *reinterpret_cast<float4*>(ks + row * L::LDK + col) = kq[i];
-      *reinterpret_cast<float4*>(vs + row * L::LDV + col) = vq[i];
+      for (int db = 0; db < NDB; ++db) tl.v[r][db] = load_one<T>(v_rs, (uint32_t)((key * D + db * 32 + lq) * ES));
     }
-    __syncthreads();
-    if (j0 >= wave_kv_end) continue;  // causal: no key of this tile is visible to this wave
+  };
 
-    f32x16 s[NKB];
+  auto compute = [&](const Tile& tl, int j0) {
+    f32x16 s = f32x16{};
 #pragma unroll
-    for (int b = 0; b < NKB; ++b) {
-      s[b] = f32x16{};
+    for (int kk = 0; kk < HALF; ++kk) s = mfma32x32x2(tl.k[kk], qf[kk], s);
+    if (j0 + BN > N || (causal && j0 + BN - 1 > q0)) {
 #pragma unroll
-      for (int u = 0; u < HALF / 4; ++u) {
-        const float4 kf = *reinterpret_cast<const float4*>(ks + (b * 32 + lq) * L::LDK + hi * HALF + 4 * u);
-        s[b] = mfma32x32x2(kf.x, qf[4 * u + 0], s[b]);
-        s[b] = mfma32x32x2(kf.y, qf[4 * u + 1], s[b]);
-        s[b] = mfma32x32x2(kf.z, qf[4 * u + 2], s[b]);
-        s[b] = mfma32x32x2(kf.w, qf[4 * u + 3], s[b]);
+      for (int r = 0; r < 16; ++r) {
+        const int key = j0 + 8 * (r / 4) + 4 * hi + (r % 4);
+        if (key >= N || (causal && key > qrow)) s[r] = -INFINITY;
       }
     }
-
-    const bool need_mask = (j0 + BN > N) || (causal && j0 + BN - 1 > q0w);
-    if (need_mask) {
-#pragma unroll
-      for (int b = 0; b < NKB; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = j0 + b * 32 + (r / 4) * 8 + hi * 4 + (r % 4);
-          if (key >= N || (causal && key > qrow)) s[b][r] = -INFINITY;
-        }
-    }
-
     float mx = -INFINITY;
 #pragma unroll
-    for (int b = 0; b < NKB; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-    mx = half_max(mx);
-    const float m_new = fmaxf(m_run, mx);
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    const float m_new = fmaxf(m_run, half_max(mx));
     // A row whose keys are all masked so far keeps l = 0 and O = 0 (the reference skips the
     // update, /root/reference/csrc/kernels/fused.cuh:78); alpha = 0 and P = 0 give the same
     // state without a lane-divergent branch around the MFMAs.
@@ -147,33 +152,70 @@ fa_f32_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict
     l_run *= alpha;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = exp2_fast(s[r] - sub_m);
+      l_run += p;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db] = mfma32x32x2(tl.v[r][db], p, o[db]);
+    }
+  };
 
-#pragma unroll
-    for (int b = 0; b < NKB; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2_fast(s[b][r] - sub_m);
-        l_run += p;
-        const int key = b * 32 + (r / 4) * 8 + hi * 4 + (r % 4);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) o[db] = mfma32x32x2(vs[key * L::LDV + db * 32 + lq], p, o[db]);
-      }
+  // This wave's tiles: wave, wave + KS, ...; the next one is loaded while the current computes.
+  if (wave < ntiles) {
+    Tile cur, nxt;
+    load_tile(cur, wave * BN);
+    for (int t = wave; t < ntiles; t += KS) {
+      const bool more = t + KS < ntiles;
+      if (more) load_tile(nxt, (t + KS) * BN);
+      compute(cur, t * BN);
+      if (more) cur = nxt;
+    }
   }
 
-  const float l_tot = half_sum(l_run);
-  const float inv = 1.f / l_tot;
+  // ---- Merge the KS partial states (m, l, O) of the 32 queries through LDS.
+  const float l_w = half_sum(l_run);
+  if (hi == 0) {
+    red_m[wave * 32 + lq] = m_run;
+    red_l[wave * 32 + lq] = l_w;
+  }
+  // Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4 w = {o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]};
+      *reinterpret_cast<f32x4*>(red_o + (wave * 32 + lq) * L::LDO + db * 32 + 8 * g4 + 4 * hi) = w;
+    }
+  __syncthreads();
+
+  float m_all = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < KS; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lq]);
+  float sc[KS];
+  float l_all = 0.f;
+#pragma unroll
+  for (int w = 0; w < KS; ++w) {
+    const float mw = red_m[w * 32 + lq];
+    sc[w] = (mw == -INFINITY) ? 0.f : exp2_fast(mw - m_all);   // a wave without visible keys adds nothing
+    l_all += sc[w] * red_l[w * 32 + lq];
+  }
+  const float inv = 1.f / l_all;
+  // Wave w finalises the (db, g4) groups w, w + KS, ... of its lanes' rows (4 dims each).
   if (qrow < N) {
     OutT* orow = O + base + (size_t)qrow * D;
+    for (int grp = wave; grp < NDB * 4; grp += KS) {
+      const int db = grp / 4, g4 = grp % 4;
+      const int dim = db * 32 + 8 * g4 + 4 * hi;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+      for (int w = 0; w < KS; ++w) acc += sc[w] * *reinterpret_cast<const f32x4*>(red_o + (w * 32 + lq) * L::LDO + dim);
+      typedef OutT OutV4 __attribute__((ext_vector_type(4)));
+      OutV4 out;
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        typedef OutT OutV4 __attribute__((ext_vector_type(4)));
-        OutV4 w;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);
-        *reinterpret_cast<OutV4*>(orow + db * 32 + g4 * 8 + hi * 4) = w;
-      }
+      for (int rr = 0; rr < 4; ++rr) out[rr] = from_f32<OutT>(acc[rr] * inv);
+      *reinterpret_cast<OutV4*>(orow + dim) = out;
+    }
   }
 }
 

@@ -266,10 +266,14 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   };
 
   if constexpr (STAGES == 2) {
-    // Prologue: K(0), V(0), K(1) into LDS; S(0) and its row max.
+    // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
+    // for short rows); S(0) and its row max.
     load_tile(k_rs, k_src, k_stage(even), 0);
     load_tile(v_rs, v_src, v_stage(even), 0);
-    if (ntiles > 1) load_tile(k_rs, k_src, k_stage(odd), BN);
+    if (ntiles > 1) {
+      load_tile(k_rs, k_src, k_stage(odd), BN);
+      load_tile(v_rs, v_src, v_stage(odd), BN);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -290,10 +294,11 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       constexpr int P = decltype(par)::value;
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
-      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1). Issued first so
-      // they have the whole iteration to land; waited for before its closing barrier.
+      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1) (V(1) came with
+      // the prologue). Issued first so they have the whole iteration to land; waited for before
+      // its closing barrier.
       if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(cur), (t + 2) * BN);
-      if (t + 1 < ntiles) load_tile(v_rs, v_src, v_stage(nxt), (t + 1) * BN);
+      if (t >= 1 && t + 1 < ntiles) load_tile(v_rs, v_src, v_stage(nxt), (t + 1) * BN);
       if (t < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);

@@ -130,15 +130,16 @@ const MfmaEntry* find_tuned(int dtype, int out_dtype, int64_t d, int br, int bc,
 }
 
 // ------------------------------------------------------------------ fused fp32 arithmetic
-constexpr int kF32BM = 64, kF32BN = 32;
+// 32 query rows per workgroup, keys split over kF32KS waves (merged through LDS at the end).
+constexpr int kF32KS = 4;
 
 template <typename T, typename OutT>
 hipError_t launch_f32(const void* q, const void* k, const void* v, void* o, int bh, int n, int causal,
                       hipStream_t stream) {
-  const int qblocks = (n + kF32BM - 1) / kF32BM;
+  const int qblocks = (n + 31) / 32;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((pa::fa_f32_fwd<T, 64, kF32BM, kF32BN, OutT>), dim3((unsigned)total), dim3(kF32BM / 32 * pa::kWave),
+  hipLaunchKernelGGL((pa::fa_f32_fwd<T, 64, kF32KS, OutT>), dim3((unsigned)total), dim3(kF32KS * pa::kWave),
                      0, stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(64), causal);
   return hipGetLastError();
