@@ -30,10 +30,25 @@ _DTYPE_CODE = {torch.float32: _native.DTYPE_F32, torch.float16: _native.DTYPE_F1
 
 
 _LDS_LIMIT: dict = {}
+_LDS_NEED: dict = {}
+# Raw handle of the current stream of a device index; torch's private accessor is ~10x cheaper
+# than building a torch.cuda.Stream object per call.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _stream_ptr(t: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        idx = t.device.index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _lds_need(key, fn, *args) -> int:
+    """LDS bytes a compiled tile needs (constant per configuration, queried once)."""
+    need = _LDS_NEED.get(key)
+    if need is None:
+        need = _LDS_NEED[key] = fn(*args)
+    return need
 
 
 def _lds_limit(t: torch.Tensor) -> int:
@@ -106,8 +121,9 @@ def fused_tuned(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool 
     _checks.check_fp16_d64_aligned("fused_tuned", q, k, v)
     _checks.check_tuned_config(br, bc)
     od = _checks.resolve_out_dtype("fused_tuned", q, out_dtype)
-    lib = _native.lib()
-    need = lib.pa_fused_tuned_lds_bytes(int(br), int(bc), int(bool(double_buffer)), 64, _native.DTYPE_F16)
+    key = ("tuned", int(br), int(bc), bool(double_buffer))
+    need = _lds_need(key, _native.lib().pa_fused_tuned_lds_bytes, int(br), int(bc), int(bool(double_buffer)), 64,
+                     _native.DTYPE_F16)
     _checks.check_lds("fused_tuned", need, _lds_limit(q), f"BR={br} BC={bc}")
     bh, n, d = _bhnd(q)
     o = torch.empty(q.shape, dtype=od, device=q.device)
@@ -134,8 +150,9 @@ def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = F
     _checks.check_inputs(q, k, v)
     _checks.check_tc(q, k, v)
     od = _checks.resolve_out_dtype("fused_tc", q, out_dtype)
-    lib = _native.lib()
-    _checks.check_lds("fused_tc", lib.pa_fused_tc_lds_bytes(q.shape[3], _DTYPE_CODE[q.dtype]), _lds_limit(q))
+    d, code = q.shape[3], _DTYPE_CODE[q.dtype]
+    need = _lds_need(("tc", d, code), _native.lib().pa_fused_tc_lds_bytes, d, code)
+    _checks.check_lds("fused_tc", need, _lds_limit(q))
     bh, n, d = _bhnd(q)
     o = torch.empty(q.shape, dtype=od, device=q.device)
     _call("pa_fused_tc_fwd", "fused_tc", q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
