@@ -72,6 +72,16 @@ def gate_tolerance(dtype: torch.dtype) -> float:
     return 1e-4 if dtype == torch.float32 else 2e-3
 
 
+def gate_error(out: torch.Tensor, ref: torch.Tensor) -> float:
+    """Max abs error against the fp32 reference. A bf16 output (an extension: the reference's
+    kernels return fp16) is also allowed its own rounding, half a bf16 ulp = 2^-9 |ref|, which
+    alone exceeds 2e-3 wherever |O| > 1 (short causal rows)."""
+    err = (out.float() - ref).abs()
+    if out.dtype == torch.bfloat16:
+        err = err - ref.abs() * 2.0 ** -9
+    return err.max().item()
+
+
 def workspace_bytes(name: str, b: int, h: int, n: int, d: int, elem: int) -> int:
     """Device bytes one call allocates: the fp32 N x N scores of the materialising paths (sdpa_math
     keeps scores and probabilities) plus the output."""
@@ -153,7 +163,7 @@ def run_point(name, q, k, v, causal, ref, args, flush_buf, row) -> dict:
     fn_raw = IMPLS[name]
     fn = lambda: fn_raw(q, k, v, causal)  # noqa: E731
     try:
-        err = (fn().float() - ref).abs().max().item() if ref is not None else float("nan")
+        err = gate_error(fn(), ref) if ref is not None else float("nan")
         if err > gate_tolerance(q.dtype):
             return dict(row, max_abs_err=f"{err:.2e}", status="wrong_result")
         iters = args.iters if name != "naive" or n <= 2048 else max(10, args.iters // 10)

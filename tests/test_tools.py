@@ -74,6 +74,16 @@ def test_summary_statistics():
     assert benchmark.summarize([2.0]) == (2.0, 2.0, 2.0)
 
 
+def test_bf16_gate_allows_only_the_outputs_rounding():
+    ref = torch.tensor([3.0, -2.5, 0.1])
+    out = ref.to(torch.bfloat16)                      # pure output rounding: passes
+    assert benchmark.gate_error(out, ref) <= benchmark.gate_tolerance(torch.bfloat16)
+    bad = (ref + torch.tensor([0.0, 0.0, 0.01])).to(torch.bfloat16)
+    assert benchmark.gate_error(bad, ref) > benchmark.gate_tolerance(torch.bfloat16)
+    out16 = ref.to(torch.float16)                     # fp16 keeps the reference's plain bar
+    assert benchmark.gate_error(out16, ref) == (out16.float() - ref).abs().max().item()
+
+
 def test_flush_buffer_exceeds_infinity_cache():
     assert benchmark.FLUSH_BYTES_MIN > 256 * 2**20
 
