@@ -155,7 +155,8 @@ def attention_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool =
 
 def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False,
                            p_dtype: str | None = None, bc: int = 64, group: int = 32,
-                           lazy_log2: float = 8.0, stats: dict | None = None) -> np.ndarray:
+                           lazy_log2: float = 8.0, stats: dict | None = None,
+                           check: str = "max") -> np.ndarray:
     """The fused MFMA kernel's arithmetic, in float32 (a model of this build, not the reference).
 
     Same log2-domain online softmax as ``attention_online``, with the two changes the kernel
@@ -166,8 +167,22 @@ def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: 
         by alpha = 2^(m_old - m_new); otherwise m is kept and P = 2^(s - m) may reach
         2^lazy_log2;
       * l sums the rounded P (the values multiplied into O).
-    ``stats``, if given, receives the largest P used and the number of rescales.
+    ``check`` selects how the lazy rescale is triggered:
+      * ``"max"`` (the fp16 kernels): the row max of each tile is compared with m before the
+        exponentials, as above;
+      * ``"rounded"`` (the bf16 kernel): the exponentials are taken against the reference
+        m_ref = m + (lazy_log2 - 1), i.e. P' = P 2^-(lazy_log2 - 1), rounded, and the rescale
+        fires when some rounded P' of the group reaches 2; then every row whose max grew takes
+        m_ref = max + lazy_log2 - 1, O and l are multiplied by 2^(m_ref_old - m_ref_new) and
+        P' is recomputed. A group's first tile always takes the exact max. m_ref starts at the
+        finite -3e38, so masked scores give P' = 0.
+    ``stats``, if given, receives the largest P used (P' scaled back by 2^(lazy_log2 - 1) for
+    ``"rounded"``) and the number of rescales.
     """
+    if check == "rounded":
+        return _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats)
+    if check != "max":
+        raise ValueError(f"unknown check {check!r}")
     q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
     *batch, n, d = q32.shape
     out = np.empty_like(q32)
@@ -207,6 +222,57 @@ def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: 
                 p_max = max(p_max, float(p_mm.max()))
             l = l * alpha + p_mm.sum(axis=-1, dtype=np.float32)
             o = o * alpha[..., None] + np.matmul(p_mm, v32[..., j0:j1, :])
+        out[..., i0:i1, :] = o / l[..., None]
+    if stats is not None:
+        stats["p_max"] = p_max
+        stats["rescales"] = rescales
+    return out
+
+
+def _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats):
+    """``attention_kernel_model(check="rounded")``: the bf16 kernel's overflow-check variant."""
+    q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
+    *batch, n, d = q32.shape
+    out = np.empty_like(q32)
+    scale_log2 = np.float32(LOG2E / np.sqrt(d))
+    kt = np.swapaxes(k32, -1, -2)
+    shift = np.float32(lazy_log2 - 1.0)
+    p_max, rescales = 0.0, 0
+    for i0 in range(0, n, group):
+        i1 = min(i0 + group, n)
+        qi = q32[..., i0:i1, :] * scale_log2
+        r = i1 - i0
+        rows = np.arange(i0, i1)
+        m_ref = np.full((*batch, r), -3.0e38, np.float32)
+        l = np.zeros((*batch, r), np.float32)
+        o = np.zeros((*batch, r, d), np.float32)
+        kv_end = min(n, i1) if causal else n
+        for t, j0 in enumerate(range(0, kv_end, bc)):
+            j1 = min(j0 + bc, n)
+            s = np.matmul(qi, kt[..., :, j0:j1])
+            if causal:
+                cols = np.arange(j0, j1)
+                s = np.where(cols[None, :] > rows[:, None], np.float32(-np.inf), s)
+
+            def exp_round(ref):
+                with np.errstate(over="ignore"):
+                    return round_to(np.exp2(s - ref[..., None]).astype(np.float32), p_dtype)
+
+            p = exp_round(m_ref)
+            fire = np.any(p >= 2, axis=(-1, -2), keepdims=False) if t else np.ones(batch, bool)
+            alpha = np.ones_like(m_ref)
+            if np.any(fire):
+                mrow = s.max(axis=-1) + shift
+                upd = fire[..., None] & (mrow > m_ref)
+                with np.errstate(invalid="ignore", over="ignore"):
+                    alpha = np.where(upd, np.exp2(m_ref - mrow), np.float32(1)).astype(np.float32)
+                m_ref = np.where(upd, mrow, m_ref).astype(np.float32)
+                rescales += int(np.sum(fire)) if t else 0
+                p = exp_round(m_ref)
+            if p.size:
+                p_max = max(p_max, float(p.max()) * 2.0 ** float(shift))
+            l = l * alpha + p.sum(axis=-1, dtype=np.float32)
+            o = o * alpha[..., None] + np.matmul(p, v32[..., j0:j1, :])
         out[..., i0:i1, :] = o / l[..., None]
     if stats is not None:
         stats["p_max"] = p_max

@@ -32,17 +32,23 @@
 //    so rows are unpadded and 16-byte chunks are XOR-swizzled per row instead: the K operand
 //    reads (ds_read_b128, 16 consecutive rows at one column) and the transposed V reads
 //    (4 rows x 4 chunks per 32 lanes) each touch all 64 banks once.
-//  * STAGES == 2 (default): software pipeline inside each wave. Iteration t runs
+//  * STAGES == 2 (default): software pipeline inside each wave. For fp16, iteration t runs
 //        phase A: MFMAs of S(t+1) = K(t+1).Q^T   interleaved with the VALU work that turns
-//                                                 S(t) into P(t) (exp2, row sum, rounding)
-//        phase B: MFMAs of O += V(t)^T.P(t)^T    interleaved with the row max of S(t+1)
+//                                                 S(t) into P(t) (exp2, rounding)
+//        phase B: MFMAs of O += V(t)^T.P(t)^T    interleaved with the row sum of P(t) and the
+//                                                 row max of S(t+1)
+//    For bf16 the row max leaves the fast path: P is computed against the stale reference
+//    max and checked for overflow past 2^8 with one OR over its packed bf16 patterns (see the
+//    bf16 branch below), and the exponentials are split evenly over the two phases (the second
+//    half of P(t) in phase A, the first half of P(t+1) in phase B), so each MFMA phase carries
+//    about the same VALU work.
 //    The interleave is fixed with scheduling-group barriers on a branch-free fast path (tile
 //    t+1 needs no mask); masked tiles (the N tail, causal diagonal) take a generic path. K and
 //    V have their own two-stage LDS rings (K is consumed one tile ahead of V); the loads of
 //    K(t+2) and V(t+1) fly during iteration t; one barrier per tile.
 //  * O and l are rescaled only in tiles where some row's max outgrew the reference max by
-//    more than 2^8 (a wave-uniform branch, rare after the first tile); on the fast path the
-//    rescale runs inside phase A, whose QK MFMAs do not touch O.
+//    more than 2^8 (a wave-uniform branch, rare after the first tile); on the fp16 fast path
+//    the rescale runs inside phase A, whose QK MFMAs do not touch O.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
 #pragma once
@@ -265,7 +271,170 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     }
   };
 
-  if constexpr (STAGES == 2) {
+  if constexpr (STAGES == 2 && std::is_same<T, bf16>::value) {
+    // bf16: overflow check instead of a row max. The exponent's reference point is
+    // m_ref = m + kShift, so the P.V operand is P' = 2^(S c - m_ref) = P 2^-kShift and
+    // "some P > 2^kLazyLog2" is "some rounded P' >= 2": bit 14 of the bf16 pattern (the top
+    // exponent bit), tested by one OR over the packed P' registers. bf16 has fp32's exponent
+    // range, so the 2^-7 scale loses nothing, and O / l is unchanged (numerator and denominator
+    // carry the same scale). When the check fires (wave-uniform, rare after the first tile) the
+    // exact row max is taken, O and l are rescaled and P'(t) is recomputed: the same update as
+    // the fp16 path, done after the exponentials instead of before them. The finite start value
+    // of m_ref makes every finite score of a row's first visible tile overflow (a rescale) and
+    // keeps a masked score at P' = 0 without a NaN.
+    constexpr float kShift = kLazyLog2 - 1.f;
+    constexpr uint32_t kTopExp = 0x40004000u;   // exponent MSB of both bf16 halves
+    constexpr int HALF = PV_STEPS / 2;
+    float m_ref = -3.0e38f;
+    // OR of the P' patterns of one operand register into the check word; the check fires when
+    // some lane of the wave has the top exponent bit set.
+    auto check_acc = [&](const V8& a, uint32_t acc) __attribute__((always_inline)) -> uint32_t {
+      const u32x4 x = __builtin_bit_cast(u32x4, a);
+      return acc | x[0] | x[1] | x[2] | x[3];
+    };
+    auto check_fires = [&](uint32_t acc) __attribute__((always_inline)) -> bool {
+      return __builtin_amdgcn_ballot_w64((acc & kTopExp) != 0) != 0;
+    };
+    // `opaque` hides -m_ref behind an empty asm so that the fast path's exponentials are not
+    // merged with the generic path's and hoisted out of the MFMA phases.
+    auto exp_range = [&](const f32x16 (&s_)[NKB], V8 (&pf)[PV_STEPS], int lo, int hi, bool opaque) __attribute__((always_inline)) {
+      float nm = -m_ref;
+      if (opaque) asm("" : "+v"(nm));
+#pragma unroll
+      for (int i = 0; i < PV_STEPS; ++i)
+        if (i >= lo && i < hi)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pf[i][j] = from_f32<T>(exp2_fast(fmaf(s_[i / 2][8 * (i % 2) + j], scale_log2, nm)));
+    };
+    // Rare path: exact row max of S(t); rows whose max grew take m_ref = max + kShift and
+    // rescale O and l by 2^(m_ref_old - m_ref_new) (0 on a row's first visible tile).
+    auto exact_rescale = [&](const f32x16 (&s_)[NKB]) __attribute__((always_inline)) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < NKB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_[b][r]);
+      const float mrow = half_max(mx) * scale_log2 + kShift;   // -inf on a fully masked row
+      const bool upd = mrow > m_ref;
+      const float alpha = upd ? exp2_fast(m_ref - mrow) : 1.f;
+      m_ref = upd ? mrow : m_ref;
+      rescale_o(alpha);
+    };
+    constexpr int c0 = 0, ch = HALF, cf = PV_STEPS;
+
+    // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
+    // for short rows); S(0).
+    load_tile(k_rs, k_src, k_stage(even), 0);
+    load_tile(v_rs, v_src, v_stage(even), 0);
+    if (ntiles > 1) {
+      load_tile(k_rs, k_src, k_stage(odd), BN);
+      load_tile(v_rs, v_src, v_stage(odd), BN);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // Score and P' buffers swap roles every iteration (the loop is unrolled by two so the swap
+    // costs no register moves). On the fast path the first HALF P' registers of tile t and
+    // their OR (`or_c`) come from iteration t-1 (for tile 0, from the prologue, after the first
+    // tile's exact max).
+    f32x16 sa[NKB], sb[NKB];
+    V8 pa[PV_STEPS], pb[PV_STEPS];
+    uint32_t or_c = kTopExp;
+    if (wave_tiles > 0) {
+      qk(sa, k_stage(even));
+      if (clean_tiles < 1) mask(sa, 0);
+      exact_rescale(sa);   // the first tile's exact max: m_ref set, O and l stay 0
+      exp_range(sa, pa, c0, ch, false);
+      uint32_t nb = 0;
+#pragma unroll
+      for (int i = 0; i < HALF; ++i) nb = check_acc(pa[i], nb);
+      or_c = nb;
+    }
+
+    // `par` is the parity of t as a compile-time constant, so every stage below is a fixed LDS
+    // object: K(t+1) in k_stage(!par), V(t) in v_stage(par).
+    auto iteration = [&](auto par, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB], V8 (&pf)[PV_STEPS],
+                         V8 (&pn)[PV_STEPS]) {
+      constexpr int P = decltype(par)::value;
+      const std::integral_constant<int, P> cur{};
+      const std::integral_constant<int, 1 - P> nxt{};
+      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1) (V(1) came with
+      // the prologue). Issued first so they have the whole iteration to land; waited for before
+      // its closing barrier.
+      if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(cur), (t + 2) * BN);
+      if (t >= 1 && t + 1 < ntiles) load_tile(v_rs, v_src, v_stage(nxt), (t + 1) * BN);
+      if (t < wave_tiles) {
+        const unsigned char* kn = k_stage(nxt);
+        const unsigned char* vc = v_stage(cur);
+        if (t + 1 < clean_tiles) {
+          // Fast path, straight-line. Phase A: S(t+1) MFMAs with the second half of P'(t) and
+          // the overflow check of all of P'(t).
+          constexpr int VA = (HALF * 20 + 6 + QK_MFMAS - 1) / QK_MFMAS;
+          constexpr int VB = (HALF * 20 + PV_STEPS * 4 + 3 + PV_MFMAS - 1) / PV_MFMAS;
+          qk(sn, kn);
+          exp_range(s, pf, ch, cf, true);
+          uint32_t bits = or_c;
+#pragma unroll
+          for (int i = HALF; i < PV_STEPS; ++i) bits = check_acc(pf[i], bits);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+          for (int i = 0; i < QK_MFMAS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, VA, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if (check_fires(bits)) {
+            exact_rescale(s);
+            exp_range(s, pf, c0, cf, false);
+          }
+          // Phase B: PV(t) MFMAs with the row sum of P'(t) and the first half of P'(t+1).
+          pv(pf, vc);
+          row_sum(pf);
+          exp_range(sn, pn, c0, ch, true);
+          uint32_t nb = 0;
+#pragma unroll
+          for (int i = 0; i < HALF; ++i) nb = check_acc(pn[i], nb);
+          or_c = nb;
+          // V operand reads (two per MFMA) run two MFMAs ahead of their use.
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+          for (int i = 0; i < PV_MFMAS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, VB, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          // Generic path: the next tile is masked or absent. P'(t) is computed here in full.
+          const bool ahead = t + 1 < wave_tiles;
+          exp_range(s, pf, c0, cf, false);
+          uint32_t bits = 0;
+#pragma unroll
+          for (int i = 0; i < PV_STEPS; ++i) bits = check_acc(pf[i], bits);
+          if (check_fires(bits)) {
+            exact_rescale(s);
+            exp_range(s, pf, c0, cf, false);
+          }
+          row_sum(pf);
+          pv(pf, vc);
+          if (ahead) {
+            qk(sn, kn);
+            mask(sn, (t + 1) * BN);
+          }
+          or_c = kTopExp;   // no P'(t+1) half was made: a fast iteration after this one recomputes
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    };
+
+    for (int t = 0; t < ntiles; t += 2) {
+      iteration(even, t, sa, sb, pa, pb);
+      if (t + 1 < ntiles) iteration(odd, t + 1, sb, sa, pb, pa);
+    }
+  } else if constexpr (STAGES == 2) {
+    // fp16: the row max of S(t+1) decides the rescale before its exponentials.
     // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
     // for short rows); S(0) and its row max.
     load_tile(k_rs, k_src, k_stage(even), 0);

@@ -205,14 +205,17 @@ def test_golden(path):
                          ids=lambda p: os.path.basename(p)[:-4])
 def test_fused_tc_matches_rounded_p_model(path):
     """Against the oracle's model of the kernel's arithmetic (64-key tiles, lazy rescale per
-    32-row wave, P rounded to the input dtype, l from the rounded P), the MFMA kernel agrees far
-    inside the gate (differences: summation order, and P values that round differently)."""
+    32-row wave with the dtype's trigger rule, P rounded to the input dtype, l from the rounded
+    P), the MFMA kernel agrees far inside the gate (differences: summation order, and P values
+    that round differently)."""
     q, k, v, o, causal, dt, z = load_golden(path)
     if q.shape[-1] not in (64, 128):
         pytest.skip("head dim not compiled for fused_tc")
     out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32).cpu().numpy()
+    # bf16 triggers the lazy rescale on the rounded P' (check="rounded"), fp16 on the row max.
     model = oracle.attention_kernel_model(q.float().cpu().numpy(), k.float().cpu().numpy(),
-                                          v.float().cpu().numpy(), causal, p_dtype=dt, bc=64, group=32)
+                                          v.float().cpu().numpy(), causal, p_dtype=dt, bc=64, group=32,
+                                          check="rounded" if dt == "bfloat16" else "max")
     # Summation order differs (MFMA vs BLAS), so a P value close to a rounding boundary can round
     # to the neighbouring fp16/bf16 value; one such flip moves O by at most ulp(p <= 1) * max|V| / l
     # with l >= 1. Peaked rows (one dominant key) expose single flips; long flat rows average them.

@@ -276,8 +276,8 @@ def test_kernel_model_keeps_p_below_the_threshold():
         assert np.abs(got - attention_naive(q, k, v)).max() < 2e-5
 
 
-@pytest.mark.parametrize("p_dtype", ["float16", "bfloat16"])
-def test_kernel_model_dominant_key_returns_its_value(p_dtype):
+@pytest.mark.parametrize("p_dtype,check", [("float16", "max"), ("bfloat16", "max"), ("bfloat16", "rounded")])
+def test_kernel_model_dominant_key_returns_its_value(p_dtype, check):
     """One key dominates each row (every other P underflows to 0) and the stale max leaves its
     P = 2^x with fractional x, not representable in p_dtype. Summing l from the rounded P
     returns that key's V exactly; summing the unrounded P (the reference's rule) would scale it
@@ -296,10 +296,69 @@ def test_kernel_model_dominant_key_returns_its_value(p_dtype):
     q = np.eye(n, d_q, dtype=np.float32)[None, None]
     k = np.zeros((1, 1, n, d_q), np.float32)
     k[0, 0, :, :n] = (s_log2 / scale_log2).T
-    got = oracle.attention_kernel_model(q, k, v, p_dtype=p_dtype, bc=32, lazy_log2=8.0)
+    got = oracle.attention_kernel_model(q, k, v, p_dtype=p_dtype, bc=32, lazy_log2=8.0, check=check)
     p40 = np.float32(2.0) ** np.float32(7.3)
     w40 = oracle.round_to(np.array([p40], np.float32), p_dtype)[0]
     want = (w40 * v[0, 0, 40] + v[0, 0, 0]) / (w40 + 1)       # keys 0 and 40 carry all mass
     np.testing.assert_allclose(got[0, 0], np.broadcast_to(want, (n, d)), rtol=2e-6, atol=2e-6)
     unrounded_l = (w40 * v[0, 0, 40] + v[0, 0, 0]) / (p40 + 1)
     assert np.abs(unrounded_l - want).max() > 1e-4
+
+
+# ---------------------------------------------------------------- 8. the bf16 kernel's overflow check
+def test_bf16_top_exponent_bit_marks_values_from_two():
+    """Every non-negative bf16 pattern up to +inf: bit 14 (the exponent's top bit) is set exactly
+    when the value is >= 2, so an OR over packed P' patterns tests "some P' >= 2"."""
+    pats = np.arange(0, 0x7F81, dtype=np.uint32)             # +0 .. +inf
+    vals = (pats << 16).view(np.float32)
+    assert np.array_equal((pats & 0x4000) != 0, vals >= 2.0)
+    # the packed form: two patterns per 32-bit word, either half
+    lo, hi = pats[:-1:2], pats[1::2]
+    word = lo | (hi << 16)
+    assert np.array_equal((word & 0x40004000) != 0, (vals[:-1:2] >= 2) | (vals[1::2] >= 2))
+
+
+def test_bf16_rounding_commutes_with_power_of_two_scale():
+    """round_bf16(x 2^-7) = round_bf16(x) 2^-7 for normal x: computing P' = P 2^-7 instead of P
+    changes no rounding, only the common scale of O and l."""
+    rng = np.random.default_rng(25)
+    x = np.concatenate([np.exp2(rng.uniform(-100, 120, 200000)),
+                        np.array([1.0, 2.0, 1.00390625, 1.005859375, 255.5, 256.0])]).astype(np.float32)
+    a = oracle.round_bf16(x * np.float32(2.0 ** -7))
+    b = oracle.round_bf16(x) * np.float32(2.0 ** -7)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [1.0, 4.0])
+def test_kernel_model_rounded_check_is_exact(causal, scale):
+    """check="rounded" with unrounded P: O / l still equals float64 softmax to float32 accuracy,
+    P stays below 2^8, and it rescales no more often than the row-max rule."""
+    rng = np.random.default_rng(26)
+    q, k, v = (rng.standard_normal((1, 2, 300, 64)).astype(np.float32) for _ in range(3))
+    q *= scale
+    st_r, st_m = {}, {}
+    got = oracle.attention_kernel_model(q, k, v, causal, lazy_log2=8.0, stats=st_r, check="rounded")
+    oracle.attention_kernel_model(q, k, v, causal, lazy_log2=8.0, stats=st_m, check="max")
+    assert np.abs(got - attention_naive(q, k, v, causal)).max() < 2e-5
+    assert st_r["p_max"] < 2.0 ** 8
+    assert st_r["rescales"] <= st_m["rescales"]
+
+
+def test_kernel_model_rounded_check_rescales_growing_rows():
+    """Scores that keep growing along the row: the rounded-P' check fires, P stays below 2^8 and
+    the result matches the reference."""
+    n, d = 512, 16
+    q = np.ones((1, 1, n, d), np.float32)
+    k = (np.linspace(0, 12, n, dtype=np.float32)[:, None] * np.ones((1, d), np.float32))[None, None]
+    v = np.random.default_rng(27).standard_normal((1, 1, n, d)).astype(np.float32)
+    st = {}
+    got = oracle.attention_kernel_model(q, k, v, lazy_log2=8.0, stats=st, check="rounded", p_dtype="bfloat16")
+    assert st["p_max"] < 2.0 ** 8 and st["rescales"] > 1
+    assert np.abs(got - attention_naive(q, k, v)).max() < 2e-3
+
+
+def test_kernel_model_rejects_unknown_check():
+    with pytest.raises(ValueError):
+        oracle.attention_kernel_model(np.zeros((1, 4, 8), np.float32), np.zeros((1, 4, 8), np.float32),
+                                      np.zeros((1, 4, 8), np.float32), check="sum")
