@@ -84,6 +84,21 @@ def test_bf16_gate_allows_only_the_outputs_rounding():
     assert benchmark.gate_error(out16, ref) == (out16.float() - ref).abs().max().item()
 
 
+def test_bf16_causal_gate_allows_one_rounded_weight():
+    """bf16 with a causal mask: the first row's single key carries all the weight; one weight
+    rounded to bf16 moves O by half a bf16 ulp of max|V|, which the causal bf16 bar admits."""
+    assert benchmark.gate_tolerance(torch.bfloat16, causal=False, vmax=4.0) == 2e-3
+    assert benchmark.gate_tolerance(torch.bfloat16, causal=True, vmax=0.5) == 2e-3
+    tol = benchmark.gate_tolerance(torch.bfloat16, causal=True, vmax=4.0)
+    assert tol == pytest.approx(1.25 * 2.0 ** -9 * 4.0)
+    # two keys, weights 0.4 / 0.6 with V = +4 / -4: rounding the weight 0.4 to bf16 moves O by
+    # 4 * 2 * |0.4 - bf16(0.4)| (both weights shift, V differs by 8), inside the bar
+    w = torch.tensor(0.4)
+    shift = 4.0 * 2 * (w - w.to(torch.bfloat16).float()).abs().item()
+    assert 2e-3 < shift <= tol
+    assert benchmark.gate_tolerance(torch.float16, causal=True, vmax=4.0) == 2e-3
+
+
 def test_flush_buffer_exceeds_infinity_cache():
     assert benchmark.FLUSH_BYTES_MIN > 256 * 2**20
 
