@@ -13,6 +13,8 @@ call a flush of a buffer larger than the 256 MB Infinity Cache, event timing, me
 and reported under "per_config". Before timing, outputs are gated against a float64 GPU reference
 on sampled heads. The CPU baseline is the oracle's NumPy restatement of the reference's online
 softmax (oracle/online_softmax.py, br=64 bc=32, P rounded to bf16) timed on a bounded sample of C4.
+"reference_workload" times fused_tc on the one shape the reference measured on hardware (A100,
+BH=324 N=128 d=64 fp16) with the reference harness's protocol and reports the ratio to its median.
 """
 from __future__ import annotations
 
@@ -118,6 +120,20 @@ def per_config(flush, iters: int):
         log(f"[per-config] {name}: {med:.4f} ms  {tf:.1f} TFLOP/s  err={err:.2e}")
         del q, k, v
     return rows
+
+
+def reference_workload():
+    """fused_tc at the reference's own measured workload (BH=324, N=128, d=64, fp16) with its
+    harness protocol (/root/reference/sim/harness.cu:146-163), beside the A100 median the reference
+    published (/root/reference/results/autotune/measured/hw_measurements.json:42-47)."""
+    sys.path.insert(0, os.path.join(REPO, "phantom-a100_amd", "bench"))
+    import reference_workload as rw
+    row = rw.measure(["fused_tc"])[0]
+    log(f"[reference workload] fused_tc BH=324 N=128: {row.get('median_ms')} ms vs A100 {row['a100_ms']} ms")
+    return {"shape": list(rw.SHAPE), "dtype": "fp16", "entry": "fused_tc", "protocol": "reference harness "
+            "(10 warm-ups, 200 launches each between two events, no flush, median)",
+            "median_ms": row.get("median_ms"), "tflops": row.get("tflops"), "max_abs_err": row["max_abs_err"],
+            "status": row["status"], "a100_median_ms": row["a100_ms"], "speedup_vs_a100": row.get("speedup_vs_a100")}
 
 
 def cpu_baseline(cfg, budget_s: float):
@@ -238,6 +254,7 @@ def main():
         flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")  # > 256 MB Infinity Cache
         out["per_config"] = per_config(flush, args.iters)
         del flush
+        out["reference_workload"] = reference_workload()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
         log(f"[cpu] {out['cpu_baseline']['sample']}: {out['cpu_baseline']['value']} TFLOP/s")

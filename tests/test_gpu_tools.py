@@ -89,3 +89,12 @@ def test_select_tiles_profiles_a_candidate(tmp_path):
         assert best.get(key) is not None, key
     assert 0 < best["mfma_util"] <= 100
     assert os.path.exists(out) and "Chosen" in open(out).read()
+
+
+def test_reference_workload_runs_the_harness_protocol():
+    """The reference's measured shape through fused_tc and one fused_tuned point: gated, timed."""
+    rw = load("pa_reference_workload", os.path.join(PKG, "bench", "reference_workload.py"))
+    rows = rw.measure(["fused_tc", "fused_vec/br128/bc32"], iters=5)
+    assert [r["status"] for r in rows] == ["ok", "ok"]
+    for r in rows:
+        assert r["median_ms"] > 0 and r["max_abs_err"] <= 2e-3 and r["speedup_vs_a100"] > 0

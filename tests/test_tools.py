@@ -30,6 +30,7 @@ def load(name, path):
 
 benchmark = load("pa_benchmark", os.path.join(PKG, "bench", "benchmark.py"))
 build_native = load("pa_build_native", os.path.join(PKG, "build_native.py"))
+rw = load("pa_reference_workload", os.path.join(PKG, "bench", "reference_workload.py"))
 
 
 # ---------------------------------------------------------------- benchmark harness
@@ -101,6 +102,37 @@ def test_bf16_causal_gate_allows_one_rounded_weight():
 
 def test_flush_buffer_exceeds_infinity_cache():
     assert benchmark.FLUSH_BYTES_MIN > 256 * 2**20
+
+
+# ---------------------------------------------------------------- the reference's measured workload
+def test_reference_workload_points_map_to_entry_points():
+    assert rw.parse_point("fused_tc") == ("fused_tc", {})
+    assert rw.parse_point("fused/br64/bc32") == ("fused", {})
+    assert rw.parse_point("fused_vec/br128/bc32/db") == ("fused_tuned", {"br": 128, "bc": 32, "double_buffer": True})
+    assert rw.parse_point("fused_vec/br64/bc64") == ("fused_tuned", {"br": 64, "bc": 64, "double_buffer": False})
+    with pytest.raises(ValueError):
+        rw.parse_point("fused/br128/bc32")            # harness-only launcher argument
+    for point in rw.A100_MS:
+        name, kw = rw.parse_point(point)
+        if name == "fused_tuned":
+            assert (kw["br"], kw["bc"]) in {(64, 32), (64, 64), (128, 32), (128, 64)}
+
+
+def test_reference_workload_flops_match_the_published_derivation():
+    """4 * 324 * 128^2 * 64 FLOP over the A100's 0.06918 ms is the 19.64 TFLOP/s derived for the
+    reference's fused_tc."""
+    assert rw.FLOPS == 1_358_954_496
+    assert round(rw.FLOPS / (rw.A100_MS["fused_tc"] * 1e-3) / 1e12, 2) == 19.64
+
+
+def test_reference_workload_report_lists_every_row():
+    rows = [{"point": "fused_tc", "entry": "fused_tc", "kwargs": {}, "max_abs_err": 1e-4, "a100_ms": 0.06918,
+             "status": "ok", "median_ms": 0.01, "min_ms": 0.009, "tflops": 135.9, "speedup_vs_a100": 6.92},
+            {"point": "naive", "entry": "naive", "kwargs": {}, "max_abs_err": 1.0, "a100_ms": 1.75677,
+             "status": "wrong_result"}]
+    text = rw.report(rows, "cmd")
+    assert "| fused_tc | fused_tc | 0.06918 | 0.01000 | 135.9 | 6.92x |" in text
+    assert "| naive | naive | 1.75677 | wrong_result |" in text
 
 
 # ---------------------------------------------------------------- counter passes and parsing
