@@ -64,10 +64,18 @@ def _bhnd(q: torch.Tensor):
     return b * h, n, d
 
 
+_FNS: dict = {}
+# Current device index without torch.cuda.current_device()'s lazy-init wrapper (the launch path
+# runs after a CUDA tensor exists, so the runtime is initialised).
+_get_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+
 def _call(fn_name: str, err_name: str, device: torch.device, *args) -> None:
     """Launch on `device` (switching the current device only when it differs)."""
-    fn = getattr(_native.lib(), fn_name)
-    if device.index is None or device.index == torch.cuda.current_device():
+    fn = _FNS.get(fn_name)
+    if fn is None:
+        fn = _FNS[fn_name] = getattr(_native.lib(), fn_name)
+    if device.index is None or device.index == _get_device():
         rc = fn(*args)
     else:
         with torch.cuda.device(device):
@@ -104,7 +112,7 @@ def fused(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = Fals
     _checks.check_float_half("fused_forward", q)
     od = _checks.resolve_out_dtype("fused_forward", q, out_dtype)
     bh, n, d = _bhnd(q)
-    o = torch.empty(q.shape, dtype=od, device=q.device)
+    o = (torch.empty_like(q) if od == q.dtype else torch.empty_like(q, dtype=od))
     _call("pa_fused_fwd", "fused_forward", q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
           _DTYPE_CODE[q.dtype], _DTYPE_CODE[od], bh, n, d, int(bool(causal)), _stream_ptr(q))
     return o
@@ -126,7 +134,7 @@ def fused_tuned(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool 
                      _native.DTYPE_F16)
     _checks.check_lds("fused_tuned", need, _lds_limit(q), f"BR={br} BC={bc}")
     bh, n, d = _bhnd(q)
-    o = torch.empty(q.shape, dtype=od, device=q.device)
+    o = (torch.empty_like(q) if od == q.dtype else torch.empty_like(q, dtype=od))
     _call("pa_fused_tuned_fwd", "fused_tuned", q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
           _native.DTYPE_F16, _DTYPE_CODE[od], bh, n, d, int(bool(causal)), int(bool(double_buffer)), int(br), int(bc),
           _stream_ptr(q))
@@ -154,7 +162,7 @@ def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = F
     need = _lds_need(("tc", d, code), _native.lib().pa_fused_tc_lds_bytes, d, code)
     _checks.check_lds("fused_tc", need, _lds_limit(q))
     bh, n, d = _bhnd(q)
-    o = torch.empty(q.shape, dtype=od, device=q.device)
+    o = (torch.empty_like(q) if od == q.dtype else torch.empty_like(q, dtype=od))
     _call("pa_fused_tc_fwd", "fused_tc", q.device, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
           _DTYPE_CODE[q.dtype], _DTYPE_CODE[od], bh, n, d, int(bool(causal)), _stream_ptr(q))
     return o
