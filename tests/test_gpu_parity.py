@@ -266,6 +266,25 @@ def test_repeat_calls_are_bitwise_identical():
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("n", [1, 15, 63, 64, 65, 200, 1000])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("qk_scale", [1.0, 3.0])
+def test_bf16_ragged_and_peaked(n, d, causal, qk_scale):
+    """The bf16 path (overflow check on the rounded P' instead of a row max) at ragged N, both head
+    dims, causal, and peaked rows (Q, K x3: frequent rescales). Against float64 with the bf16
+    P-rounding bound (short causal rows and peaked rows put most weight on a few rounded P), and
+    against the oracle's model of the same arithmetic with the rounding-flip bound."""
+    print(f"[bf16] n={n} d={d} causal={causal} qk_scale={qk_scale}", flush=True)
+    q, k, v = make_qkv(1, 3, n, d, torch.bfloat16, seed=31, qk_scale=qk_scale, device="cuda")
+    out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)
+    vmax = v.float().abs().max().item()
+    assert max_err(out, f64_reference_gpu(q, k, v, causal)) <= max(2e-3, 1.25 * 2.0 ** -9 * vmax)
+    model = oracle.attention_kernel_model(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                                          causal, p_dtype="bfloat16", bc=64, group=32, check="rounded")
+    assert np.abs(out.cpu().numpy() - model).max() <= max(2.5e-4, 2.0 ** -7 * vmax)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_c4_shape_causal_matches_float64(causal):
     """Causal at the headline bf16 / d=128 shape (4 heads): the path the non-causal bench skips."""
