@@ -104,6 +104,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   static_assert((BN * CR) % THREADS == 0, "K/V tile must split evenly over the workgroup");
   constexpr int CPT = BN * CR / THREADS; // 16-byte chunks per thread per matrix per tile
   static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
+  // Operand reads address the stages through ds_read's 16-bit immediate offset; a stage above
+  // 64 KB would need its addresses built in extra VGPRs (measured: -11 % at d = 128).
+  static_assert(L::BYTES <= 65536, "K/V stages must fit ds_read's 64 KB offset reach");
 
   // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
   // cannot alias the operand reads from another, and does not make those reads wait for it.
