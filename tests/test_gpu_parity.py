@@ -269,10 +269,11 @@ def test_repeat_calls_are_bitwise_identical():
 @pytest.mark.parametrize("n", [1, 15, 63, 64, 65, 200, 1000])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("qk_scale", [1.0, 3.0])
+@pytest.mark.parametrize("qk_scale", [1.0, 3.0, 10.0])
 def test_bf16_ragged_and_peaked(n, d, causal, qk_scale):
     """The bf16 path (overflow check on the rounded P' instead of a row max) at ragged N, both head
-    dims, causal, and peaked rows (Q, K x3: frequent rescales). Against float64 with the bf16
+    dims, causal, and peaked rows (Q, K x3 and x10: frequent rescales, and P' overflowing to inf
+    before the exact path takes over). Against float64 with the bf16
     P-rounding bound (short causal rows and peaked rows put most weight on a few rounded P), and
     against the oracle's model of the same arithmetic with the rounding-flip bound."""
     print(f"[bf16] n={n} d={d} causal={causal} qk_scale={qk_scale}", flush=True)
