@@ -1,0 +1,94 @@
+"""Seeded random parity sweep of every entry point against a float64 softmax(QK^T/sqrt(d))V.
+
+The reference's suite (tests/test_correctness.py) fixes B=2, H=4, d=64 and a list of N; this sweep
+draws the shape (B, H, N, d), causal, the input dtype and the output dtype per case from one fixed
+seed, within what each entry point accepts, so that shapes between the fixed ones (odd head
+counts, N just past a tile, d = 32/80 for the unfused paths, fp32 outputs) are also exercised.
+Bars: fp32 inputs 1e-4 (the reference's), fp16 2e-3, bf16 max(2e-3, 1.25 * 2^-9 * max|V|) (a few
+rounded P can carry a short causal row), each plus half an ulp of the output dtype.
+"""
+from __future__ import annotations
+
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import cuda_attn
+from cuda_attn.workloads import make_qkv
+
+pytestmark = pytest.mark.gpu
+
+ENTRIES = {
+    # name: (input dtypes, head dims, takes out_dtype)
+    "naive": ((torch.float32, torch.float16), (32, 64, 80, 128), False),
+    "tiled": ((torch.float32, torch.float16), (32, 64, 80, 128), False),
+    "fused": ((torch.float32, torch.float16), (64,), True),
+    "fused_vec": ((torch.float16,), (64,), False),
+    "fused_db": ((torch.float16,), (64,), False),
+    "fused_tuned": ((torch.float16,), (64,), True),
+    "fused_tc": ((torch.float16, torch.bfloat16), (64, 128), True),
+}
+TILES = ((64, 32), (64, 64), (128, 32), (128, 64))
+
+
+def draw_cases(count: int = 180, seed: int = 2026):
+    rng = random.Random(seed)
+    names = list(ENTRIES)
+    cases = []
+    for i in range(count):
+        name = names[i % len(names)]
+        dtypes, dims, takes_out = ENTRIES[name]
+        dtype = rng.choice(dtypes)
+        d = rng.choice(dims)
+        n_max = 1500 if name in ("naive", "tiled") else 2500
+        n = max(1, int(round(math.exp(rng.uniform(0.0, math.log(n_max))))))
+        kw = {}
+        if name == "fused_tuned":
+            br, bc = rng.choice(TILES)
+            kw = {"br": br, "bc": bc, "double_buffer": rng.random() < 0.5}
+        out_dtype = torch.float32 if takes_out and rng.random() < 0.4 else None
+        cases.append(dict(name=name, b=rng.randint(1, 3), h=rng.randint(1, 5), n=n, d=d, dtype=dtype,
+                          causal=rng.random() < 0.5, out_dtype=out_dtype, kw=kw, seed=1000 + i))
+    return cases
+
+
+def f64_reference(q, k, v, causal):
+    b, h, n, d = q.shape
+    qf, kf, vf = (t.reshape(b * h, n, d).double() for t in (q, k, v))
+    out = torch.empty((b * h, n, d), dtype=torch.float64, device=q.device)
+    for i0 in range(0, b * h, 4):
+        s = torch.matmul(qf[i0:i0 + 4], kf[i0:i0 + 4].transpose(1, 2).contiguous()) / math.sqrt(d)
+        if causal:
+            s.masked_fill_(torch.ones(n, n, dtype=torch.bool, device=q.device).triu(1), float("-inf"))
+        out[i0:i0 + 4] = torch.matmul(torch.softmax(s, dim=-1), vf[i0:i0 + 4])
+    return out.reshape(b, h, n, d)
+
+
+def case_id(c):
+    return (f"{c['name']}-{str(c['dtype'])[6:]}-b{c['b']}h{c['h']}n{c['n']}d{c['d']}"
+            f"{'-causal' if c['causal'] else ''}{'-f32out' if c['out_dtype'] is not None else ''}")
+
+
+@pytest.mark.parametrize("case", draw_cases(), ids=case_id)
+def test_random_shape_matches_float64(case):
+    c = case
+    print(f"[fuzz] {case_id(c)} {c['kw']}", flush=True)
+    q, k, v = make_qkv(c["b"], c["h"], c["n"], c["d"], c["dtype"], seed=c["seed"], device="cuda")
+    fn = getattr(cuda_attn, c["name"])
+    kwargs = dict(c["kw"])
+    if c["out_dtype"] is not None:
+        kwargs["out_dtype"] = c["out_dtype"]
+    out = fn(q, k, v, c["causal"], **kwargs)
+    want_dtype = c["out_dtype"] or c["dtype"]
+    assert out.shape == q.shape and out.dtype == want_dtype
+    ref = f64_reference(q, k, v, c["causal"])
+    vmax = v.float().abs().max().item()
+    bar = {torch.float32: 1e-4, torch.float16: 2e-3}.get(c["dtype"])
+    if c["dtype"] == torch.bfloat16:
+        bar = max(2e-3, 1.25 * 2.0 ** -9 * vmax)
+    bar += 0.5 * torch.finfo(want_dtype).eps * ref.abs().max().item()
+    err = (out.double() - ref).abs().max().item()
+    assert np.isfinite(err) and err <= bar, f"{case_id(c)}: max abs error {err:.3e} > {bar:.3e}"
