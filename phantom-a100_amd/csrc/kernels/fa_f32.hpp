@@ -9,7 +9,10 @@
 //   O^T (d x queries)   += V^T . P^T  B = P^T straight from the S^T accumulator (k-slot h of
 //                                    step r = key 8*(r/4) + 4*h + r%4), A = V (lane: one dim of
 //                                    the two keys of the step)
-// Each lane keeps all state of query l%32 (see fa_mfma.hpp).
+// Each lane keeps all state of query l%32 (see fa_mfma.hpp). Row i of the two 32-row O^T blocks
+// is dim 2i (block 0) and dim 2i + 1 (block 1), so each lane reads the V values of both blocks
+// with one 8-byte load (fp32; 4 bytes for fp16) instead of two scalar loads; the merge puts the
+// dims back in order.
 //
 // gfx950 shape: the fp32 matrix core does 64 FLOP per cycle per SIMD, so a 32-query x 32-key
 // tile costs a wave ~4K cycles; at the reference's sizes (N = 128) a wave per 32 queries leaves
@@ -61,6 +64,21 @@ __device__ __forceinline__ float load_one(rsrc_t rs, uint32_t byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, byte_off, 0, 0));
   } else {
     return (float)__builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(rs, byte_off, 0, 0));
+  }
+}
+
+// Two consecutive elements of a row, widened to fp32 (offsets past the buffer read as zero).
+template <typename T>
+__device__ __forceinline__ void load_pair(rsrc_t rs, uint32_t byte_off, float& a, float& b) {
+  if constexpr (sizeof(T) == 4) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 w = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, byte_off, 0, 0));
+    a = w[0];
+    b = w[1];
+  } else {
+    const f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_raw_buffer_load_b32(rs, byte_off, 0, 0));
+    a = (float)h[0];
+    b = (float)h[1];
   }
 }
 
@@ -122,8 +140,7 @@ fa_f32_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = j0 + 8 * (r / 4) + 4 * hi + (r % 4);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) tl.v[r][db] = load_one<T>(v_rs, (uint32_t)((key * D + db * 32 + lq) * ES));
+      load_pair<T>(v_rs, (uint32_t)((key * D + 2 * lq) * ES), tl.v[r][0], tl.v[r][1]);   // dims 2 lq, 2 lq + 1
     }
   };
 
@@ -179,14 +196,16 @@ fa_f32_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict
     red_m[wave * 32 + lq] = m_run;
     red_l[wave * 32 + lq] = l_w;
   }
-  // Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
+  // Register r of block db holds row i = 8*(r/4) + 4*hi + r%4, i.e. dim 2i + db: registers
+  // 4 g4 .. 4 g4 + 3 of both blocks are the 8 consecutive dims 16 g4 + 8 hi .. + 7.
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const f32x4 w = {o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]};
-      *reinterpret_cast<f32x4*>(red_o + (wave * 32 + lq) * L::LDO + db * 32 + 8 * g4 + 4 * hi) = w;
-    }
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const f32x4 w0 = {o[0][4 * g4], o[1][4 * g4], o[0][4 * g4 + 1], o[1][4 * g4 + 1]};
+    const f32x4 w1 = {o[0][4 * g4 + 2], o[1][4 * g4 + 2], o[0][4 * g4 + 3], o[1][4 * g4 + 3]};
+    float* dst = red_o + (wave * 32 + lq) * L::LDO + 16 * g4 + 8 * hi;
+    *reinterpret_cast<f32x4*>(dst) = w0;
+    *reinterpret_cast<f32x4*>(dst + 4) = w1;
+  }
   __syncthreads();
 
   float m_all = -INFINITY;
