@@ -56,9 +56,10 @@ def candidates(entry: str, d: int):
     return [(f"br{br}_bc{bc}_{st}stage", br, bc, st)]
 
 
-def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dtype: torch.dtype) -> str:
-    """Fragment of the mangled name of pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT>."""
-    return f"fa_mfma_fwdI{MANGLED_T[dtype]}Li{d}ELi{br}ELi{bc}ELi{stages}E{MANGLED_T[out_dtype]}E"
+def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dtype: torch.dtype,
+               ksplit: int = 1) -> str:
+    """Fragment of the mangled name of pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT>."""
+    return f"fa_mfma_fwdI{MANGLED_T[dtype]}Li{d}ELi{br}ELi{bc}ELi{stages}E{MANGLED_T[out_dtype]}Li{ksplit}EE"
 
 
 def load_resources(path: str = RESOURCES) -> dict:

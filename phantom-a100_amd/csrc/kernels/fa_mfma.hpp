@@ -49,6 +49,11 @@
 //  * O and l are rescaled only in tiles where some row's max outgrew the reference max by
 //    more than 2^8 (a wave-uniform branch, rare after the first tile); on the fp16 fast path
 //    the rescale runs inside phase A, whose QK MFMAs do not touch O.
+//  * KSPLIT == 2 (short rows on a small grid): the workgroup's waves form two key groups; group
+//    g walks the key tiles g, g + 2, ... through its own half of every LDS stage, with its own
+//    (m, l, O), so each wave walks half the tiles. At the end group 1 hands (m, l, O) to the
+//    lane of group 0 holding the same query and dims, through the freed stages, and group 0
+//    merges them with the online-softmax rule and stores.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
 #pragma once
@@ -82,8 +87,8 @@ template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 1
 #define PA_MFMA_OCCUPANCY
 #endif
 
-template <typename T, int D, int BM, int BN, int STAGES, typename OutT>
-__global__ void __launch_bounds__(BM / 32 * kWave) PA_MFMA_OCCUPANCY
+template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1>
+__global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT) PA_MFMA_OCCUPANCY
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
   typedef typename vec8<T>::type V8;
@@ -106,22 +111,33 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
   // Operand reads address the stages through ds_read's 16-bit immediate offset; a stage above
   // 64 KB would need its addresses built in extra VGPRs (measured: -11 % at d = 128).
-  static_assert(L::BYTES <= 65536, "K/V stages must fit ds_read's 64 KB offset reach");
+  static_assert(L::BYTES * KSPLIT <= 65536, "K/V stages must fit ds_read's 64 KB offset reach");
+  static_assert(KSPLIT == 1 || (KSPLIT == 2 && STAGES == 2 && (BM / 32) % 2 == 0),
+                "key groups: two-stage pipeline, an even number of query waves");
 
   // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
   // cannot alias the operand reads from another, and does not make those reads wait for it.
-  __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[L::TILE_BYTES];
-  __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[L::TILE_BYTES];
-  __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[STAGES == 2 ? L::TILE_BYTES : 16];
-  __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[STAGES == 2 ? L::TILE_BYTES : 16];
-  auto k_stage = [&](auto par) -> unsigned char* { if constexpr (decltype(par)::value) return k_lds1; else return k_lds0; };
-  auto v_stage = [&](auto par) -> unsigned char* { if constexpr (decltype(par)::value) return v_lds1; else return v_lds0; };
+  // With KSPLIT key groups each object holds one tile per group.
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[L::TILE_BYTES * KSPLIT];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[L::TILE_BYTES * KSPLIT];
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[STAGES == 2 ? L::TILE_BYTES * KSPLIT : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[STAGES == 2 ? L::TILE_BYTES * KSPLIT : 16];
   const std::integral_constant<int, 0> even{};
   const std::integral_constant<int, 1> odd{};
 
-  const int tid = threadIdx.x;
+  // Waves are (key group g) x (query wave): group g takes the key tiles g, g + KSPLIT, ...
+  const int g = KSPLIT == 1 ? 0 : (int)threadIdx.x / THREADS;
+  const int tid = KSPLIT == 1 ? (int)threadIdx.x : (int)threadIdx.x % THREADS;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
+  auto k_stage = [&](auto par) -> unsigned char* {
+    if constexpr (decltype(par)::value) return k_lds1 + g * L::TILE_BYTES; else return k_lds0 + g * L::TILE_BYTES;
+  };
+  auto v_stage = [&](auto par) -> unsigned char* {
+    if constexpr (decltype(par)::value) return v_lds1 + g * L::TILE_BYTES; else return v_lds0 + g * L::TILE_BYTES;
+  };
+  // Key tile of this group's iteration j.
+  auto tile_of = [&](int j) { return j * KSPLIT + g; };
   const int lq = lane % 32;   // query column of this lane in the wave's 32-query tile
   const int hi = lane / 32;   // which half of the 32 accumulator rows this lane holds
 
@@ -181,6 +197,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     v_addr[db] = v_row * RB + (((4 * db + v_cl) ^ v_swz<CR>(v_row)) * 16) + 8 * (i16 % 2);
 
   float m_run = -INFINITY;  // running max of the log2-domain scores of row qrow
+  float m_out = -INFINITY;  // the exponent reference O and l are scaled by, for the key-group merge
   float l_run = 0.f;        // running sum over the 16 keys per 32 held by this lane
   f32x16 o[NDB];
 #pragma unroll
@@ -188,6 +205,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 
   const int kv_end = causal ? min(N, q0 + BM) : N;
   const int ntiles = (kv_end + BN - 1) / BN;
+  const int nit = (ntiles + KSPLIT - 1) / KSPLIT;   // iterations of every key group
   const int wave_kv_end = causal ? min(kv_end, q0w + 32) : kv_end;  // keys this wave can see
   const int wave_tiles = (wave_kv_end + BN - 1) / BN;
   // Tiles [0, clean_tiles) need no mask for this wave: all keys < N and (causal) all keys at or
@@ -327,11 +345,13 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 
     // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
     // for short rows); S(0).
-    load_tile(k_rs, k_src, k_stage(even), 0);
-    load_tile(v_rs, v_src, v_stage(even), 0);
-    if (ntiles > 1) {
-      load_tile(k_rs, k_src, k_stage(odd), BN);
-      load_tile(v_rs, v_src, v_stage(odd), BN);
+    if (KSPLIT == 1 || tile_of(0) < ntiles) {   // a workgroup always has a first tile
+      load_tile(k_rs, k_src, k_stage(even), tile_of(0) * BN);
+      load_tile(v_rs, v_src, v_stage(even), tile_of(0) * BN);
+    }
+    if (tile_of(1) < ntiles) {
+      load_tile(k_rs, k_src, k_stage(odd), tile_of(1) * BN);
+      load_tile(v_rs, v_src, v_stage(odd), tile_of(1) * BN);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -343,9 +363,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     f32x16 sa[NKB], sb[NKB];
     V8 pa[PV_STEPS], pb[PV_STEPS];
     uint32_t or_c = kTopExp;
-    if (wave_tiles > 0) {
+    if (tile_of(0) < wave_tiles) {
       qk(sa, k_stage(even));
-      if (clean_tiles < 1) mask(sa, 0);
+      if (tile_of(0) >= clean_tiles) mask(sa, tile_of(0) * BN);
       exact_rescale(sa);   // the first tile's exact max: m_ref set, O and l stay 0
       exp_range(sa, pa, c0, ch, false);
       uint32_t nb = 0;
@@ -364,12 +384,12 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1) (V(1) came with
       // the prologue). Issued first so they have the whole iteration to land; waited for before
       // its closing barrier.
-      if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(cur), (t + 2) * BN);
-      if (t >= 1 && t + 1 < ntiles) load_tile(v_rs, v_src, v_stage(nxt), (t + 1) * BN);
-      if (t < wave_tiles) {
+      if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
+      if (t >= 1 && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
+      if (tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
-        if (t + 1 < clean_tiles) {
+        if (tile_of(t + 1) < clean_tiles) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the second half of P'(t) and
           // the overflow check of all of P'(t).
           constexpr int VA = (HALF * 20 + 6 + QK_MFMAS - 1) / QK_MFMAS;
@@ -410,7 +430,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           __builtin_amdgcn_sched_barrier(0);
         } else {
           // Generic path: the next tile is masked or absent. P'(t) is computed here in full.
-          const bool ahead = t + 1 < wave_tiles;
+          const bool ahead = tile_of(t + 1) < wave_tiles;
           exp_range(s, pf, c0, cf, false);
           uint32_t bits = 0;
 #pragma unroll
@@ -423,7 +443,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
-            mask(sn, (t + 1) * BN);
+            mask(sn, tile_of(t + 1) * BN);
           }
           or_c = kTopExp;   // no P'(t+1) half was made: a fast iteration after this one recomputes
         }
@@ -432,19 +452,22 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       __syncthreads();
     };
 
-    for (int t = 0; t < ntiles; t += 2) {
+    for (int t = 0; t < nit; t += 2) {
       iteration(even, t, sa, sb, pa, pb);
-      if (t + 1 < ntiles) iteration(odd, t + 1, sb, sa, pb, pa);
+      if (t + 1 < nit) iteration(odd, t + 1, sb, sa, pb, pa);
     }
+    m_out = m_ref;
   } else if constexpr (STAGES == 2) {
     // fp16: the row max of S(t+1) decides the rescale before its exponentials.
     // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
     // for short rows); S(0) and its row max.
-    load_tile(k_rs, k_src, k_stage(even), 0);
-    load_tile(v_rs, v_src, v_stage(even), 0);
-    if (ntiles > 1) {
-      load_tile(k_rs, k_src, k_stage(odd), BN);
-      load_tile(v_rs, v_src, v_stage(odd), BN);
+    if (KSPLIT == 1 || tile_of(0) < ntiles) {   // a workgroup always has a first tile
+      load_tile(k_rs, k_src, k_stage(even), tile_of(0) * BN);
+      load_tile(v_rs, v_src, v_stage(even), tile_of(0) * BN);
+    }
+    if (tile_of(1) < ntiles) {
+      load_tile(k_rs, k_src, k_stage(odd), tile_of(1) * BN);
+      load_tile(v_rs, v_src, v_stage(odd), tile_of(1) * BN);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -454,9 +477,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     f32x16 sa[NKB], sb[NKB];
     bool rescale = false;
     float alpha = 1.f;
-    if (wave_tiles > 0) {
+    if (tile_of(0) < wave_tiles) {
       qk(sa, k_stage(even));
-      if (clean_tiles < 1) mask(sa, 0);
+      if (tile_of(0) >= clean_tiles) mask(sa, tile_of(0) * BN);
       alpha = update_max(sa, rescale);
     }
 
@@ -469,13 +492,13 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1) (V(1) came with
       // the prologue). Issued first so they have the whole iteration to land; waited for before
       // its closing barrier.
-      if (t + 2 < ntiles) load_tile(k_rs, k_src, k_stage(cur), (t + 2) * BN);
-      if (t >= 1 && t + 1 < ntiles) load_tile(v_rs, v_src, v_stage(nxt), (t + 1) * BN);
-      if (t < wave_tiles) {
+      if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
+      if (t >= 1 && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
+      if (tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
         V8 pf[PV_STEPS];
-        if (t + 1 < clean_tiles) {
+        if (tile_of(t + 1) < clean_tiles) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/round of S(t) and,
           // if m moved, the rescale of O and l. Two copies so the common case carries no muls.
           auto phase_a = [&](auto with_rescale) {
@@ -510,14 +533,14 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           __builtin_amdgcn_sched_barrier(0);
         } else {
           // Generic path: the next tile is masked or absent.
-          const bool ahead = t + 1 < wave_tiles;
+          const bool ahead = tile_of(t + 1) < wave_tiles;
           if (rescale) rescale_o(alpha);
           exponentiate(s, pf);
           row_sum(pf);
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
-            mask(sn, (t + 1) * BN);
+            mask(sn, tile_of(t + 1) * BN);
             alpha = update_max(sn, rescale);
           }
         }
@@ -526,10 +549,11 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       __syncthreads();
     };
 
-    for (int t = 0; t < ntiles; t += 2) {
+    for (int t = 0; t < nit; t += 2) {
       iteration(even, t, sa, sb);
-      if (t + 1 < ntiles) iteration(odd, t + 1, sb, sa);
+      if (t + 1 < nit) iteration(odd, t + 1, sb, sa);
     }
+    m_out = m_run;
   } else {
     for (int t = 0; t < ntiles; ++t) {
       const int j0 = t * BN;
@@ -553,10 +577,40 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     }
   }
 
+  // ---- Key groups: group 1 hands (m, l, O) to the lane of group 0 that holds the same query and
+  // dims, through the (now free) K/V stages; group 0 merges them with the online-softmax rule
+  // (m = max, l and O scaled by 2^(m_g - m); a group that saw no key of the row adds nothing).
+  if constexpr (KSPLIT == 2) {
+    static_assert(NW * NDB * 16 * kWave * 4 <= 2 * L::TILE_BYTES * KSPLIT, "merge fits two stages");
+    __syncthreads();   // every group is done with the stages
+    float* red_o = reinterpret_cast<float*>(wave < NW / 2 ? k_lds0 : v_lds0) + (wave % (NW / 2)) * (NDB * 16 * kWave);
+    float* red_ml = reinterpret_cast<float*>(k_lds1) + wave * 2 * kWave;
+    if (g == 1) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red_o[(db * 16 + r) * kWave + lane] = o[db][r];
+      red_ml[lane] = m_out;
+      red_ml[kWave + lane] = l_run;
+    }
+    __syncthreads();
+    if (g == 0) {
+      const float m1 = red_ml[lane], l1 = red_ml[kWave + lane];
+      const float m = fmaxf(m_out, m1);
+      const float sc0 = (m_out == -INFINITY) ? 0.f : exp2_fast(m_out - m);
+      const float sc1 = (m1 == -INFINITY) ? 0.f : exp2_fast(m1 - m);
+      l_run = sc0 * l_run + sc1 * l1;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] = sc0 * o[db][r] + sc1 * red_o[(db * 16 + r) * kWave + lane];
+    }
+  }
+
   // ---- Epilogue: O = O^T / l. Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
   const float l_tot = half_sum(l_run);
   const float inv = 1.f / l_tot;
-  if (qrow < N) {
+  if (g == 0 && qrow < N) {
     OutT* orow = O + base + (size_t)qrow * D;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)

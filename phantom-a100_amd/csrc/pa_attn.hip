@@ -69,13 +69,13 @@ int check_aligned16(const char* name, const void* q, const void* k, const void* 
 float scale_log2_for(int64_t d) { return pa::kLog2e / sqrtf((float)d); }
 
 // ------------------------------------------------------------------ fused MFMA (fp16 / bf16)
-template <typename T, int D, int BM, int BN, int ST, typename OutT>
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1>
 hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int bh, int n, int causal,
                        hipStream_t stream) {
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT>), dim3((unsigned)total), dim3(BM / 32 * pa::kWave), 0,
+  hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS>), dim3((unsigned)total), dim3(BM / 32 * pa::kWave * KS), 0,
                      stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);
   return hipGetLastError();
@@ -84,7 +84,7 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
 typedef hipError_t (*mfma_fn)(const void*, const void*, const void*, void*, int, int, int, hipStream_t);
 
 struct MfmaEntry {
-  int dtype, out_dtype, d, br, bc, db;
+  int dtype, out_dtype, d, br, bc, db, ks;
   mfma_fn fn;
   int64_t lds;
 };
@@ -94,13 +94,14 @@ template <> constexpr int dt_code<pa::f16>() { return PA_DTYPE_F16; }
 template <> constexpr int dt_code<pa::bf16>() { return PA_DTYPE_BF16; }
 template <> constexpr int dt_code<float>() { return PA_DTYPE_F32; }
 
-template <typename T, int D, int BM, int BN, int ST, typename OutT>
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1>
 constexpr MfmaEntry mfma_entry() {
-  return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, &launch_mfma<T, D, BM, BN, ST, OutT>,
-                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES};
+  return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, KS, &launch_mfma<T, D, BM, BN, ST, OutT, KS>,
+                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS};
 }
 
 #define PA_TC_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T>(), mfma_entry<T, D, BM, BN, ST, float>()
+#define PA_TC_SPLIT_BOTH_OUT(T, D, BM, BN) mfma_entry<T, D, BM, BN, 2, T, 2>(), mfma_entry<T, D, BM, BN, 2, float, 2>()
 
 // fused_tc: one tile configuration per (dtype, d), chosen by measurement on MI355X. d = 128
 // uses 8 waves (256 queries) per workgroup: one workgroup per CU, so each K/V tile is staged
@@ -112,12 +113,28 @@ const MfmaEntry kTcTable[] = {
     PA_TC_BOTH_OUT(pa::f16, 128, 256, 64, 2),
     PA_TC_BOTH_OUT(pa::bf16, 128, 256, 64, 2),
 };
+// Short rows on a small grid (d = 64, 2-4 key tiles, at most one workgroup per CU): 64-query
+// workgroups whose keys are split over two groups of 2 waves, so each wave walks half the tiles
+// and the extra waves land on otherwise idle CUs; the groups merge at the end. Measured at
+// BH = 42: N = 128 7.76 vs 8.44 us, N = 256 9.48 vs 10.16 us; slower with one tile, longer rows or
+// a grid that already fills the chip.
+constexpr int kCUs = 256;   // MI355X / gfx950
+const MfmaEntry kTcSplitTable[] = {
+    PA_TC_SPLIT_BOTH_OUT(pa::f16, 64, 64, 64),
+    PA_TC_SPLIT_BOTH_OUT(pa::bf16, 64, 64, 64),
+};
+bool use_key_split(int64_t d, int64_t n, int64_t bh) {
+  return d == 64 && n > 64 && n <= 256 && (n + 63) / 64 * bh <= kCUs;
+}
 
 // fused_tuned: the reference's tile sweep set (fused_tuned.cuh:207) x {one, two} LDS stages.
 #define PA_TUNED(BR, BC) PA_TC_BOTH_OUT(pa::f16, 64, BR, BC, 1), PA_TC_BOTH_OUT(pa::f16, 64, BR, BC, 2)
 const MfmaEntry kTunedTable[] = {PA_TUNED(64, 32), PA_TUNED(64, 64), PA_TUNED(128, 32), PA_TUNED(128, 64)};
 
-const MfmaEntry* find_tc(int dtype, int out_dtype, int64_t d) {
+const MfmaEntry* find_tc(int dtype, int out_dtype, int64_t d, int64_t n, int64_t bh) {
+  if (use_key_split(d, n, bh))
+    for (const auto& e : kTcSplitTable)
+      if (e.dtype == dtype && e.out_dtype == out_dtype && e.d == d) return &e;
   for (const auto& e : kTcTable)
     if (e.dtype == dtype && e.out_dtype == out_dtype && e.d == d) return &e;
   return nullptr;
@@ -255,7 +272,7 @@ int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o, int dt
     return fail(PA_ERR_UNSUPPORTED, "%s: only head dimensions 64 and 128 are compiled (got %lld)", name, (long long)d);
   if (int rc = check_aligned16(name, q, k, v, o)) return rc;
   if (int rc = check_head_bytes(name, n, d, dtype)) return rc;
-  const MfmaEntry* e = find_tc(dtype, out_dtype, d);
+  const MfmaEntry* e = find_tc(dtype, out_dtype, d, n, bh);
   if (!e) return fail(PA_ERR_UNSUPPORTED, "%s: output dtype must be the input dtype or float32", name);
   return hip_status(e->fn(q, k, v, o, (int)bh, (int)n, causal, static_cast<hipStream_t>(stream)), name);
 }
@@ -266,8 +283,11 @@ int64_t pa_fused_tuned_lds_bytes(int br, int bc, int double_buffer, int64_t d, i
 }
 
 int64_t pa_fused_tc_lds_bytes(int64_t d, int dtype) {
-  const MfmaEntry* e = find_tc(dtype, dtype, d);
-  return e ? e->lds : -1;
+  // the larger of the general and the short-row (key-split) tile
+  const MfmaEntry* e = find_tc(dtype, dtype, d, 1 << 20, 1);
+  const MfmaEntry* s = find_tc(dtype, dtype, d, 128, 1);
+  if (!e) return -1;
+  return s && s->lds > e->lds ? s->lds : e->lds;
 }
 
 int pa_device_lds_limit(int device, int64_t* bytes) {

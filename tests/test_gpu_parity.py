@@ -286,6 +286,25 @@ def test_bf16_ragged_and_peaked(n, d, causal, qk_scale):
     assert np.abs(out.cpu().numpy() - model).max() <= max(2.5e-4, 2.0 ** -7 * vmax)
 
 
+@pytest.mark.parametrize("n", [65, 128, 200, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_key_split_matches_unsplit(n, dtype, causal):
+    """d = 64 rows of 2-4 key tiles on a small grid take the key-split kernel (two key groups
+    merged at the end); the same heads inside a 300-head batch take the unsplit one. Both match
+    float64, and each other to within P rounding."""
+    print(f"[key split] n={n} {dtype} causal={causal}", flush=True)
+    q, k, v = make_qkv(1, 300, n, 64, dtype, seed=41, device="cuda")
+    big = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)[:, :3]
+    qs, ks, vs = (t[:, :3].contiguous() for t in (q, k, v))
+    small = cuda_attn.fused_tc(qs, ks, vs, causal, out_dtype=torch.float32)
+    ref = f64_reference_gpu(qs, ks, vs, causal)
+    vmax = vs.float().abs().max().item()
+    tol = 2e-3 if dtype == torch.float16 else max(2e-3, 1.25 * 2.0 ** -9 * vmax)
+    assert max_err(small, ref) <= tol and max_err(big, ref) <= tol
+    assert max_err(small, big) <= tol
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_c4_shape_causal_matches_float64(causal):
     """Causal at the headline bf16 / d=128 shape (4 heads): the path the non-causal bench skips."""
