@@ -373,6 +373,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       for (int i = 0; i < HALF; ++i) nb = check_acc(pa[i], nb);
       or_c = nb;
     }
+    // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first.
+    __syncthreads();
 
     // `par` is the parity of t as a compile-time constant, so every stage below is a fixed LDS
     // object: K(t+1) in k_stage(!par), V(t) in v_stage(par).
@@ -381,9 +383,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       constexpr int P = decltype(par)::value;
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
-      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1) (V(1) came with
-      // the prologue). Issued first so they have the whole iteration to land; waited for before
-      // its closing barrier.
+      // K(t+2) replaces K(t) (read in iteration t-1; K(0) by the first tile, before the barrier
+      // above); V(t+1) replaces V(t-1) (V(1) came with the prologue). Issued first so they have
+      // the whole iteration to land; waited for before its closing barrier.
       if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
       if (t >= 1 && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
       if (tile_of(t) < wave_tiles) {
@@ -482,6 +484,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       if (tile_of(0) >= clean_tiles) mask(sa, tile_of(0) * BN);
       alpha = update_max(sa, rescale);
     }
+    // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first.
+    __syncthreads();
 
     // `par` is the parity of t as a compile-time constant, so every stage below is a fixed LDS
     // object: K(t+1) in k_stage(!par), V(t) in v_stage(par).
@@ -489,9 +493,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       constexpr int P = decltype(par)::value;
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
-      // K(t+2) replaces K(t) (read in iteration t-1); V(t+1) replaces V(t-1) (V(1) came with
-      // the prologue). Issued first so they have the whole iteration to land; waited for before
-      // its closing barrier.
+      // K(t+2) replaces K(t) (read in iteration t-1; K(0) by the first tile, before the barrier
+      // above); V(t+1) replaces V(t-1) (V(1) came with the prologue). Issued first so they have
+      // the whole iteration to land; waited for before its closing barrier.
       if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
       if (t >= 1 && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
       if (tile_of(t) < wave_tiles) {
