@@ -266,6 +266,29 @@ def test_repeat_calls_are_bitwise_identical():
     assert torch.equal(a, b)
 
 
+# Every LDS-pipelined kernel form: the two-stage bf16 and fp16 paths at both head dims, the key
+# split, causal rows and fused_tuned's prefetching tiles. The kernels have no atomics and a fixed
+# reduction order, so repeated launches must agree bit for bit; an LDS stage overwritten while
+# another wave still reads it would show up as run-to-run differences.
+@pytest.mark.parametrize("name, shape, dtype, causal, kw", [
+    ("fused_tc", (2, 16, 2048, 128), torch.bfloat16, False, {}),
+    ("fused_tc", (2, 16, 2048, 128), torch.float16, True, {}),
+    ("fused_tc", (4, 16, 1024, 64), torch.float16, False, {}),
+    ("fused_tc", (4, 16, 1024, 64), torch.bfloat16, True, {}),
+    ("fused_tc", (1, 42, 128, 64), torch.float16, False, {}),      # key split
+    ("fused_tc", (1, 42, 256, 64), torch.bfloat16, True, {}),      # key split, causal
+    ("fused_tuned", (2, 8, 1024, 64), torch.float16, False, {"br": 128, "bc": 64, "double_buffer": True}),
+    ("fused_tuned", (2, 8, 1000, 64), torch.float16, True, {"br": 64, "bc": 32, "double_buffer": True}),
+])
+def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
+    print(f"[repeat] {name} {shape} {dtype} causal={causal} {kw}", flush=True)
+    q, k, v = make_qkv(*shape, dtype, seed=11, device="cuda")
+    fn = getattr(cuda_attn, name)
+    first = fn(q, k, v, causal, **kw)
+    for _ in range(10):
+        assert torch.equal(fn(q, k, v, causal, **kw), first)
+
+
 @pytest.mark.parametrize("n", [1, 15, 63, 64, 65, 200, 1000])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
