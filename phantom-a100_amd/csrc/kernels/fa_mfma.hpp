@@ -33,10 +33,10 @@
 //    reads (ds_read_b128, 16 consecutive rows at one column) and the transposed V reads
 //    (4 rows x 4 chunks per 32 lanes) each touch all 64 banks once.
 //  * STAGES == 2 (default): software pipeline inside each wave. For fp16, iteration t runs
-//        phase A: MFMAs of S(t+1) = K(t+1).Q^T   interleaved with the VALU work that turns
-//                                                 S(t) into P(t) (exp2, rounding)
-//        phase B: MFMAs of O += V(t)^T.P(t)^T    interleaved with the row sum of P(t) and the
-//                                                 row max of S(t+1)
+//        phase A: MFMAs of S(t+1) = K(t+1).Q^T   interleaved with the VALU work that turns the
+//                                                 second half of S(t) into P(t) (exp2, rounding)
+//        phase B: MFMAs of O += V(t)^T.P(t)^T    interleaved with the row sum of P(t), the row
+//                                                 max of S(t+1) and the first half of P(t+1)
 //    For bf16 the row max leaves the fast path: P is computed against the stale reference
 //    max and checked for overflow past 2^8 with one OR over its packed bf16 patterns (see the
 //    bf16 branch below), and the exponentials are split evenly over the two phases (the second
@@ -477,19 +477,35 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     // Two score buffers swap roles every iteration (the loop is unrolled by two so the swap
     // costs no register moves).
     f32x16 sa[NKB], sb[NKB];
+    V8 pa[PV_STEPS], pb[PV_STEPS];
     bool rescale = false;
     float alpha = 1.f;
+    // The first QB P operand registers of tile t+1 are made in phase B of iteration t, right after
+    // its row max, the rest in phase A of iteration t+1, so both MFMA phases carry about the same
+    // VALU work. `opaque` keeps the fast path's exponentials from being merged with the generic
+    // path's and hoisted out of the MFMA phases.
+    constexpr int QB = PV_STEPS / 2;
+    auto exp_part = [&](const f32x16 (&s_)[NKB], V8 (&p_)[PV_STEPS], int lo, int hi, bool opaque) __attribute__((always_inline)) {
+      float nm = (m_run == -INFINITY) ? 0.f : -m_run;  // fully masked row: P = 0
+      if (opaque) asm("" : "+v"(nm));
+#pragma unroll
+      for (int i = 0; i < PV_STEPS; ++i)
+        if (i >= lo && i < hi)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) p_[i][j] = from_f32<T>(exp2_fast(fmaf(s_[i / 2][8 * (i % 2) + j], scale_log2, nm)));
+    };
     if (tile_of(0) < wave_tiles) {
       qk(sa, k_stage(even));
       if (tile_of(0) >= clean_tiles) mask(sa, tile_of(0) * BN);
       alpha = update_max(sa, rescale);
+      exp_part(sa, pa, 0, QB, false);
     }
     // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first.
     __syncthreads();
 
     // `par` is the parity of t as a compile-time constant, so every stage below is a fixed LDS
     // object: K(t+1) in k_stage(!par), V(t) in v_stage(par).
-    auto iteration = [&](auto par, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB]) {
+    auto iteration = [&](auto par, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB], V8 (&pf)[PV_STEPS], V8 (&pn)[PV_STEPS]) {
       constexpr int P = decltype(par)::value;
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
@@ -501,51 +517,54 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       if (tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
-        V8 pf[PV_STEPS];
         if (tile_of(t + 1) < clean_tiles) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/round of S(t) and,
           // if m moved, the rescale of O and l. Two copies so the common case carries no muls.
           auto phase_a = [&](auto with_rescale) {
             constexpr bool RS = decltype(with_rescale)::value;
+            constexpr int VA = ((PV_STEPS - QB) * 20 + (RS ? NDB * 16 + 2 : 0) + QK_MFMAS - 1) / QK_MFMAS;
             qk(sn, kn);
             if constexpr (RS) rescale_o(alpha);
-            exponentiate(s, pf);
+            exp_part(s, pf, QB, PV_STEPS, true);
             // K operand reads run two MFMAs ahead of their use.
             __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
 #pragma unroll
             for (int i = 0; i < QK_MFMAS; ++i) {
               __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
               __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-              __builtin_amdgcn_sched_group_barrier(kSchedValu, RS ? 9 : 5, 0);
+              __builtin_amdgcn_sched_group_barrier(kSchedValu, VA, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
           };
           if (rescale) phase_a(std::true_type{});
           else phase_a(std::false_type{});
           // Phase B: PV(t) MFMAs with the row sum of P(t) and the row max of S(t+1).
+          constexpr int VB = (PV_STEPS * 4 + NKB * 8 + 10 + QB * 20 + PV_MFMAS - 1) / PV_MFMAS;
           pv(pf, vc);
           row_sum(pf);
           alpha = update_max(sn, rescale);
+          exp_part(sn, pn, 0, QB, true);
           // V operand reads (two per MFMA) run two MFMAs ahead of their use.
           __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
           for (int i = 0; i < PV_MFMAS; ++i) {
             __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
             __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, VB, 0);
           }
           __builtin_amdgcn_sched_barrier(0);
         } else {
           // Generic path: the next tile is masked or absent.
           const bool ahead = tile_of(t + 1) < wave_tiles;
           if (rescale) rescale_o(alpha);
-          exponentiate(s, pf);
+          exp_part(s, pf, QB, PV_STEPS, false);
           row_sum(pf);
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
             mask(sn, tile_of(t + 1) * BN);
             alpha = update_max(sn, rescale);
+            exp_part(sn, pn, 0, QB, false);
           }
         }
       }
@@ -554,8 +573,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     };
 
     for (int t = 0; t < nit; t += 2) {
-      iteration(even, t, sa, sb);
-      if (t + 1 < nit) iteration(odd, t + 1, sb, sa);
+      iteration(even, t, sa, sb, pa, pb);
+      if (t + 1 < nit) iteration(odd, t + 1, sb, sa, pb, pa);
     }
     m_out = m_run;
   } else {
