@@ -33,10 +33,12 @@
 //    reads (ds_read_b128, 16 consecutive rows at one column) and the transposed V reads
 //    (4 rows x 4 chunks per 32 lanes) each touch all 64 banks once.
 //  * STAGES == 2 (default): software pipeline inside each wave. For fp16, iteration t runs
-//        phase A: MFMAs of S(t+1) = K(t+1).Q^T   interleaved with the VALU work that turns the
-//                                                 second half of S(t) into P(t) (exp2, rounding)
+//        phase A: MFMAs of S(t+1) = K(t+1).Q^T   interleaved with the VALU work that turns S(t)
+//                                                 into P(t) (exp2, rounding; at d = 64 only its
+//                                                 second half)
 //        phase B: MFMAs of O += V(t)^T.P(t)^T    interleaved with the row sum of P(t), the row
-//                                                 max of S(t+1) and the first half of P(t+1)
+//                                                 max of S(t+1) and, at d = 64, the first half
+//                                                 of P(t+1)
 //    For bf16 the row max leaves the fast path: P is computed against the stale reference
 //    max and checked for overflow past 2^8 with one OR over its packed bf16 patterns (see the
 //    bf16 branch below), and the exponentials are split evenly over the two phases (the second
@@ -483,10 +485,10 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     // The first QB P operand registers of tile t+1 are made in phase B of iteration t, right after
     // its row max, the rest in phase A of iteration t+1, so both MFMA phases carry about the same
     // VALU work. `opaque` keeps the fast path's exponentials from being merged with the generic
-    // path's and hoisted out of the MFMA phases. Measured per tile: the 64 x 64 tile (2 waves,
-    // 64-key tiles) runs 6 % faster with all of P(t) in phase A (QB = 0), every other tile 2-7 %
-    // faster with the split.
-    constexpr int QB = (BM == 64 && BN == 64) ? 0 : PV_STEPS / 2;
+    // path's and hoisted out of the MFMA phases. Measured per tile: at d = 64 every tile but the
+    // 64 x 64 one runs 2-7 % faster with the split; that tile (6 %) and d = 128 (1 %, where 16
+    // MFMAs per phase already carry the exponentials) run faster with all of P(t) in phase A.
+    constexpr int QB = (D == 128 || (BM == 64 && BN == 64)) ? 0 : PV_STEPS / 2;
     auto exp_part = [&](const f32x16 (&s_)[NKB], V8 (&p_)[PV_STEPS], int lo, int hi, bool opaque) __attribute__((always_inline)) {
       float nm = (m_run == -INFINITY) ? 0.f : -m_run;  // fully masked row: P = 0
       if (opaque) asm("" : "+v"(nm));
