@@ -1,0 +1,91 @@
+"""Stream contract of the drop-in package (reference: launches go to the caller's current stream,
+asynchronously, `attn_*.cu`; here `cuda_attn` passes `torch.cuda.current_stream()` to the C ABI).
+
+* Launches on several side streams at once give the same bits as on the default stream (no
+  shared mutable state in the library).
+* A launch consumes inputs produced on the same side stream just before it, with no extra sync.
+* The fused entry points can be captured in a HIP graph; every replay (with new inputs copied in
+  eagerly between replays) matches the eager result bit for bit.
+All streams keep the default priority.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import cuda_attn
+from cuda_attn.workloads import make_qkv
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    ("fused_tc", (2, 8, 512, 128), torch.bfloat16, {}),
+    ("fused_tc", (2, 8, 1000, 64), torch.float16, {}),
+    ("fused_tuned", (1, 8, 512, 64), torch.float16, {"br": 128, "bc": 64, "double_buffer": True}),
+    ("fused", (1, 8, 256, 64), torch.float32, {}),
+    ("tiled", (1, 4, 256, 64), torch.float32, {}),
+]
+
+
+@pytest.mark.parametrize("name, shape, dtype, kw", CASES, ids=[c[0] + "-" + str(c[2])[6:] for c in CASES])
+def test_side_streams_match_default_stream(name, shape, dtype, kw):
+    print(f"[streams] {name} {shape} {dtype}", flush=True)
+    fn = getattr(cuda_attn, name)
+    inputs = [make_qkv(*shape, dtype, seed=60 + i, device="cuda") for i in range(3)]
+    want = [fn(q, k, v, False, **kw) for q, k, v in inputs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in inputs]
+    got = [None] * len(inputs)
+    for _ in range(3):
+        for i, ((q, k, v), s) in enumerate(zip(inputs, streams)):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                got[i] = fn(q, k, v, False, **kw)
+        for s in streams:
+            torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        for g, w in zip(got, want):
+            assert torch.equal(g, w)
+
+
+def test_launch_uses_the_current_stream():
+    """Inputs written on a side stream right before the call are the ones the kernel reads."""
+    q, k, v = make_qkv(2, 8, 1024, 128, torch.bfloat16, seed=71, device="cuda")
+    want = cuda_attn.fused_tc(q, k, v)
+    s = torch.cuda.Stream()
+    for trial in range(5):
+        q2 = torch.empty_like(q)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            torch.cuda._sleep(2_000_000)          # keep the side stream busy before the copy
+            q2.copy_(q)
+            out = cuda_attn.fused_tc(q2, k, v)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"trial {trial}"
+
+
+@pytest.mark.parametrize("name, shape, dtype, kw", CASES[:4], ids=[c[0] + "-" + str(c[2])[6:] for c in CASES[:4]])
+def test_graph_capture_replays_match_eager(name, shape, dtype, kw):
+    print(f"[graph] {name} {shape} {dtype}", flush=True)
+    fn = getattr(cuda_attn, name)
+    q, k, v = (t.clone() for t in make_qkv(*shape, dtype, seed=80, device="cuda"))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):                    # warm-up outside the graph, as torch requires
+        fn(q, k, v, False, **kw)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn(q, k, v, False, **kw)
+    for replay in range(4):
+        nq, nk, nv = make_qkv(*shape, dtype, seed=90 + replay, device="cuda")
+        q.copy_(nq)
+        k.copy_(nk)
+        v.copy_(nv)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = fn(nq, nk, nv, False, **kw)        # eager, between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {replay}"
