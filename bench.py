@@ -242,7 +242,7 @@ def main():
                      "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s",
                      "frac": round(flops / (ms_step * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 5),
                      "traffic": traffic_from_profile() if cfg.name == HEADLINE else None,
-                     "kernel": "pa::fa_mfma_fwd<bf16, D=128, BM=256, BN=64, 2 stages>",
+                     "kernel": "pa::fa_mfma_fwd<bf16, D=128, BM=256, BN=64, 2 stages, persistent: one workgroup per CU>",
                      "flops_per_launch": flops},
         "gate_max_abs_err": float(f"{err:.3e}"),
         "library": _native.version(),

@@ -58,6 +58,14 @@
 //    merges them with the online-softmax rule and stores.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
+//  * PERSIST (bf16, two stages, no key split; launched only for non-causal rows whose every key
+//    tile is full and whose tile count is even): one workgroup per CU walks the query blocks of
+//    its XCD's range. The last two iterations of a block are separate copies of the iteration
+//    (compile-time WRAP) whose loads past the block's last tile fetch the next block's K(0),
+//    K(1), V(0) and Q, so a block starts with its first tiles already in LDS and the per-block
+//    start-up (workgroup launch, first loads) is hidden behind the previous block. With every
+//    tile clean the mask code is compiled out and all but a block's last iteration take the
+//    fast path without a runtime test.
 #pragma once
 
 #include <type_traits>
@@ -89,7 +97,7 @@ template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 1
 #define PA_MFMA_OCCUPANCY
 #endif
 
-template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1>
+template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false>
 __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT) PA_MFMA_OCCUPANCY
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
@@ -116,6 +124,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   static_assert(L::BYTES * KSPLIT <= 65536, "K/V stages must fit ds_read's 64 KB offset reach");
   static_assert(KSPLIT == 1 || (KSPLIT == 2 && STAGES == 2 && (BM / 32) % 2 == 0),
                 "key groups: two-stage pipeline, an even number of query waves");
+  static_assert(!PERSIST || (KSPLIT == 1 && STAGES == 2 && std::is_same<T, bf16>::value),
+                "persistent form: bf16, two stages, no key split");
 
   // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
   // cannot alias the operand reads from another, and does not make those reads wait for it.
@@ -143,25 +153,40 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   const int lq = lane % 32;   // query column of this lane in the wave's 32-query tile
   const int hi = lane / 32;   // which half of the 32 accumulator rows this lane holds
 
-  const int blk = xcd_remap(blockIdx.x, total_blocks);
-  const int bh = blk / num_qblocks;
+  // Query block blk = (head, BM-query block). The persistent form walks the blocks of its XCD's
+  // range (blk = x * range + c + C * j for the c-th of the C workgroups on XCD x), so that all
+  // blocks of a head still run on one XCD.
+  const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
+  int blk = 0, blk_step = 0, blk_end = 0;
+  if constexpr (PERSIST) {
+    const int range = (total_blocks + kNumXcd - 1) / kNumXcd;
+    const int x = (int)blockIdx.x % kNumXcd;
+    blk_step = (int)gridDim.x / kNumXcd;
+    blk_end = min(total_blocks, (x + 1) * range);
+    blk = x * range + (int)blockIdx.x / kNumXcd;
+    if (blk >= blk_end) return;   // more workgroups than blocks on this XCD
+  } else {
+    blk = xcd_remap(blockIdx.x, total_blocks);
+  }
   int qb = blk % num_qblocks;
   if (causal) qb = num_qblocks - 1 - qb;  // longest causal rows first
-  const int q0 = qb * BM;
-  const int q0w = q0 + wave * 32;
-  const int qrow = q0w + lq;
-  const size_t base = (size_t)bh * N * D;
-  const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
-  const rsrc_t q_rs = make_rsrc(Q + base, head_bytes);
-  const rsrc_t k_rs = make_rsrc(K + base, head_bytes);
-  const rsrc_t v_rs = make_rsrc(V + base, head_bytes);
+  int q0 = qb * BM;
+  int q0w = q0 + wave * 32;
+  int qrow = q0w + lq;
+  size_t base = (size_t)(blk / num_qblocks) * N * D;
+  rsrc_t q_rs = make_rsrc(Q + base, head_bytes);
+  rsrc_t k_rs = make_rsrc(K + base, head_bytes);
+  rsrc_t v_rs = make_rsrc(V + base, head_bytes);
 
   // ---- Q^T operand: lane holds Q[qrow][16*kk + 8*hi + j], j < 8, for every k-step kk
   // (rows past N read as zero).
   V8 qf[QK_STEPS];
+  auto load_q = [&](rsrc_t rs, int row) {
 #pragma unroll
-  for (int kk = 0; kk < QK_STEPS; ++kk)
-    qf[kk] = __builtin_bit_cast(V8, load16(q_rs, (uint32_t)(qrow * RB + kk * 32 + hi * 16)));
+    for (int kk = 0; kk < QK_STEPS; ++kk)
+      qf[kk] = __builtin_bit_cast(V8, load16(rs, (uint32_t)(row * RB + kk * 32 + hi * 16)));
+  };
+  load_q(q_rs, qrow);
 
   // ---- Direct HBM -> LDS loads. Load i of this thread fills LDS slot i*THREADS + tid of the
   // tile (16 bytes each, slots in lane order), i.e. row slot/CR at physical chunk slot%CR, which
@@ -294,6 +319,25 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     }
   };
 
+  // O = O^T / l for the current block. Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
+  auto store_block = [&]() {
+    const float l_tot = half_sum(l_run);
+    const float inv = 1.f / l_tot;
+    if (g == 0 && qrow < N) {
+      OutT* orow = O + base + (size_t)qrow * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          typedef OutT OutV4 __attribute__((ext_vector_type(4)));
+          OutV4 w;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);
+          *reinterpret_cast<OutV4*>(orow + db * 32 + g4 * 8 + hi * 4) = w;
+        }
+    }
+  };
+
   if constexpr (STAGES == 2 && std::is_same<T, bf16>::value) {
     // bf16: overflow check instead of a row max. The exponent's reference point is
     // m_ref = m + kShift, so the P.V operand is P' = 2^(S c - m_ref) = P 2^-kShift and
@@ -365,24 +409,39 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     f32x16 sa[NKB], sb[NKB];
     V8 pa[PV_STEPS], pb[PV_STEPS];
     uint32_t or_c = kTopExp;
-    if (tile_of(0) < wave_tiles) {
-      qk(sa, k_stage(even));
-      if (tile_of(0) >= clean_tiles) mask(sa, tile_of(0) * BN);
-      exact_rescale(sa);   // the first tile's exact max: m_ref set, O and l stay 0
-      exp_range(sa, pa, c0, ch, false);
-      uint32_t nb = 0;
+    // S(0) and the first half of P'(0) of a block (the arrays are parameters, not captures:
+    // capturing them here changes how the compiler allocates the whole kernel).
+    auto first_tile = [&](f32x16 (&s0)[NKB], V8 (&p0)[PV_STEPS]) {
+      if (tile_of(0) < wave_tiles) {
+        qk(s0, k_stage(even));
+        if (!PERSIST && tile_of(0) >= clean_tiles) mask(s0, tile_of(0) * BN);
+        exact_rescale(s0);   // the first tile's exact max: m_ref set, O and l stay 0
+        exp_range(s0, p0, c0, ch, false);
+        uint32_t nb = 0;
 #pragma unroll
-      for (int i = 0; i < HALF; ++i) nb = check_acc(pa[i], nb);
-      or_c = nb;
-    }
+        for (int i = 0; i < HALF; ++i) nb = check_acc(p0[i], nb);
+        or_c = nb;
+      }
+    };
+    first_tile(sa, pa);
     // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first.
     __syncthreads();
+    // Persistent form: whether this workgroup has a next query block, and its index. The current
+    // block's last two iterations (the "wrap" copies) load that block's K(0), K(1), V(0) and Q.
+    bool has_next = false;
+    int blk_n = 0;
+    auto next_base = [&]() { return (size_t)(blk_n / num_qblocks) * N * D; };
 
     // `par` is the parity of t as a compile-time constant, so every stage below is a fixed LDS
     // object: K(t+1) in k_stage(!par), V(t) in v_stage(par).
-    auto iteration = [&](auto par, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB], V8 (&pf)[PV_STEPS],
+    auto iteration = [&](auto par, auto wrap, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB], V8 (&pf)[PV_STEPS],
                          V8 (&pn)[PV_STEPS]) {
       constexpr int P = decltype(par)::value;
+      // WRAP: the persistent form's last two iterations of a block (t = nit-2, nit-1): loads past
+      // the block's last tile fetch the next block's first tiles instead; the last one has no
+      // S(t+1) and therefore no fast-path copy.
+      constexpr bool WRAP = decltype(wrap)::value;
+      constexpr bool kMayBeFast = !(WRAP && P == 1);
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
       // K(t+2) replaces K(t) (read in iteration t-1; K(0) by the first tile, before the barrier
@@ -390,15 +449,21 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       // share of both loads in every iteration: on the fast path inside phase A (so the 8 waves
       // leaving the barrier do not queue them all at once; +1.4 % on C4), otherwise here. They
       // are waited for before the iteration's closing barrier.
-      const bool fast = tile_of(t) < wave_tiles && tile_of(t + 1) < clean_tiles;
+      // Persistent form: every tile is clean, so all but the last iteration take the fast path.
+      const bool fast = PERSIST ? kMayBeFast : (tile_of(t) < wave_tiles && tile_of(t + 1) < clean_tiles);
       if (!fast) {
         if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
+        else if (WRAP && has_next) load_tile(make_rsrc(K + next_base(), head_bytes), k_src, k_stage(cur), (tile_of(t + 2) - ntiles) * BN);
         if (t >= 1 && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
+        else if (WRAP && has_next && tile_of(t + 1) == ntiles) load_tile(make_rsrc(V + next_base(), head_bytes), v_src, v_stage(nxt), 0);
+        if constexpr (WRAP && P == 1) {
+          if (has_next) load_q(make_rsrc(Q + next_base(), head_bytes), (blk_n % num_qblocks) * BM + wave * 32 + lq);
+        }
       }
-      if (tile_of(t) < wave_tiles) {
+      if (PERSIST || tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
-        if (tile_of(t + 1) < clean_tiles) {
+        if (fast) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the second half of P'(t) and
           // the overflow check of all of P'(t).
           // VALU instructions placed after each MFMA: the per-phase totals spread evenly, except
@@ -409,7 +474,13 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           // This iteration's tile loads, issued inside phase A (unconditionally, to keep the phase
           // branch-free: past the last tile K reloads the last tile into the free stage, and at
           // t = 0 V(1) is written again over itself).
-          load_tile(k_rs, k_src, k_stage(cur), min(tile_of(t + 2), ntiles - 1) * BN);
+          if constexpr (WRAP) {
+            // t = nit-2: K(t+2) is the next block's K(0) (or, after the last block, this block's
+            // last tile again into the free stage).
+            load_tile(make_rsrc(K + (has_next ? next_base() : base), head_bytes), k_src, k_stage(cur), has_next ? 0 : (ntiles - 1) * BN);
+          } else {
+            load_tile(k_rs, k_src, k_stage(cur), min(tile_of(t + 2), ntiles - 1) * BN);
+          }
           load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
           exp_range(s, pf, ch, cf, true);
           uint32_t bits = or_c;
@@ -459,7 +530,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
-            mask(sn, tile_of(t + 1) * BN);
+            if constexpr (!PERSIST) mask(sn, tile_of(t + 1) * BN);
           }
           or_c = kTopExp;   // no P'(t+1) half was made: a fast iteration after this one recomputes
         }
@@ -468,9 +539,45 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       __syncthreads();
     };
 
-    for (int t = 0; t < nit; t += 2) {
-      iteration(even, t, sa, sb, pa, pb);
-      if (t + 1 < nit) iteration(odd, t + 1, sb, sa, pb, pa);
+    const std::false_type no_wrap{};
+    if constexpr (!PERSIST) {
+      for (int t = 0; t < nit; t += 2) {
+        iteration(even, no_wrap, t, sa, sb, pa, pb);
+        if (t + 1 < nit) iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+      }
+    } else {
+      // The launcher guarantees a non-causal launch whose N is a multiple of 2 * BN: every tile
+      // is clean and nit = ntiles is even (>= 2), so the block's last two iterations are the
+      // wrap copies and the query block is blk % num_qblocks.
+      const std::true_type with_wrap{};
+      while (true) {
+        blk_n = blk + blk_step;
+        has_next = blk_n < blk_end;
+        for (int t = 0; t < nit - 2; t += 2) {
+          iteration(even, no_wrap, t, sa, sb, pa, pb);
+          iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+        }
+        iteration(even, with_wrap, nit - 2, sa, sb, pa, pb);
+        iteration(odd, with_wrap, nit - 1, sb, sa, pb, pa);
+        store_block();
+        if (!has_next) break;
+        blk = blk_n;
+        q0 = (blk % num_qblocks) * BM;
+        q0w = q0 + wave * 32;
+        qrow = q0w + lq;
+        base = (size_t)(blk / num_qblocks) * N * D;
+        q_rs = make_rsrc(Q + base, head_bytes);
+        k_rs = make_rsrc(K + base, head_bytes);
+        v_rs = make_rsrc(V + base, head_bytes);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
+        l_run = 0.f;
+        m_ref = -3.0e38f;
+        // K(0), K(1), V(0) and Q landed with the last iteration's wait; V(1) comes with
+        // iteration 0's phase A, as for the first block.
+        first_tile(sa, pa);
+        __syncthreads();
+      }
     }
     m_out = m_ref;
   } else if constexpr (STAGES == 2) {
@@ -646,22 +753,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     }
   }
 
-  // ---- Epilogue: O = O^T / l. Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
-  const float l_tot = half_sum(l_run);
-  const float inv = 1.f / l_tot;
-  if (g == 0 && qrow < N) {
-    OutT* orow = O + base + (size_t)qrow * D;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        typedef OutT OutV4 __attribute__((ext_vector_type(4)));
-        OutV4 w;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);
-        *reinterpret_cast<OutV4*>(orow + db * 32 + g4 * 8 + hi * 4) = w;
-      }
-  }
+  // ---- Epilogue (the persistent form stores each block where it ends).
+  if constexpr (!PERSIST) store_block();
 }
 
 }  // namespace pa

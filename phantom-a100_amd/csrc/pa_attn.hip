@@ -8,10 +8,13 @@
 // thread-local message.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 
 #include "phantom_attn.h"
@@ -69,12 +72,50 @@ int check_aligned16(const char* name, const void* q, const void* k, const void* 
 float scale_log2_for(int64_t d) { return pa::kLog2e / sqrtf((float)d); }
 
 // ------------------------------------------------------------------ fused MFMA (fp16 / bf16)
+// Compute units of the current device (looked up once per device), 0 if unknown.
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The persistent bf16 d = 128 launch is on unless the environment sets PA_PERSISTENT=0 (read at
+// every launch, so a process can compare both forms).
+bool persistent_enabled() {
+  const char* e = getenv("PA_PERSISTENT");
+  return !(e && e[0] == '0');
+}
+
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1>
 hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int bh, int n, int causal,
                        hipStream_t stream) {
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
+  // bf16, d = 128, non-causal, N a multiple of two key tiles: the persistent form, one 8-wave
+  // workgroup per CU (its registers allow one per CU) walking the query blocks of its XCD, so the
+  // next block's first tiles load during the current block's last two. Measured on MI355X at
+  // B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024: 1184 / 1247 / 1126 / 1049
+  // against 1125 / 1198 / 1062 / 929 TFLOP/s with one workgroup per query block.
+  if constexpr (std::is_same<T, pa::bf16>::value && D == 128 && ST == 2 && KS == 1) {
+    if (!causal && n % (2 * BN) == 0 && persistent_enabled()) {
+      const long long per_xcd = (total + pa::kNumXcd - 1) / pa::kNumXcd;
+      const int grid = (int)std::min<long long>(device_cus() / pa::kNumXcd, per_xcd) * pa::kNumXcd;
+      if (grid > 0) {
+        hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true>), dim3((unsigned)grid),
+                           dim3(BM / 32 * pa::kWave * KS), 0, stream, static_cast<const T*>(q),
+                           static_cast<const T*>(k), static_cast<const T*>(v), static_cast<OutT*>(o), n,
+                           qblocks, (int)total, scale_log2_for(D), causal);
+        return hipGetLastError();
+      }
+    }
+  }
   hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS>), dim3((unsigned)total), dim3(BM / 32 * pa::kWave * KS), 0,
                      stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);

@@ -289,6 +289,40 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
         assert torch.equal(fn(q, k, v, causal, **kw), first)
 
 
+# The persistent bf16 d=128 launch (non-causal, N a multiple of 128: one workgroup per CU walking
+# its XCD's query blocks, the next block's first tiles loaded during the current block's last two
+# iterations) runs the same arithmetic in the same order as the one-workgroup-per-block launch
+# (PA_PERSISTENT=0), so the two agree bit for bit. Shapes: 8 blocks per workgroup (C4), 2 per
+# workgroup, a block count not divisible by the 8 XCDs, fewer blocks than CUs, two key tiles per
+# row (no regular iteration between the wrap copies), N = 8192, and peaked rows that rescale
+# inside the wrap iterations.
+@pytest.mark.parametrize("shape, qk_scale, out_dtype", [
+    ((4, 32, 4096), 1.0, None),
+    ((1, 64, 2048), 1.0, torch.float32),
+    ((1, 33, 4096), 1.0, None),
+    ((1, 5, 1024), 1.0, torch.float32),
+    ((1, 304, 128), 1.0, None),
+    ((2, 16, 8192), 1.0, None),
+    ((2, 40, 1024), 10.0, torch.float32),
+])
+def test_persistent_form_matches_per_block_form(shape, qk_scale, out_dtype, monkeypatch):
+    print(f"[persistent] {shape} qk_scale={qk_scale} out={out_dtype}", flush=True)
+    q, k, v = make_qkv(*shape, 128, torch.bfloat16, seed=41, qk_scale=qk_scale, device="cuda")
+    monkeypatch.delenv("PA_PERSISTENT", raising=False)
+    got = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
+    monkeypatch.setenv("PA_PERSISTENT", "0")
+    want = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    b, h, n = shape
+    heads = sorted({0, b * h // 2, b * h - 1})
+    qh, kh, vh = (t.reshape(1, b * h, n, 128)[:, heads] for t in (q, k, v))
+    ref = f64_reference_gpu(qh, kh, vh)
+    vmax = v.float().abs().max().item()
+    assert max_err(got.reshape(1, b * h, n, 128)[:, heads], ref) <= max(2e-3, 1.25 * 2.0 ** -9 * vmax) + (
+        0.5 * torch.finfo(got.dtype).eps * ref.abs().max().item())
+
+
 @pytest.mark.parametrize("n", [1, 15, 63, 64, 65, 200, 1000])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])

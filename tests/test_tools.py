@@ -223,8 +223,8 @@ def resources_fixture():
 def test_parse_resource_remarks():
     res = resources_fixture()
     assert len(res) == 5
-    c4 = [v for k, v in res.items() if "fa_mfma_fwdIDF16bLi128ELi256ELi64ELi2EDF16b" in k][0]
-    assert c4["vgprs"] == 238 and c4["agprs"] == 0 and c4["lds_bytes"] == 65536
+    c4 = [v for k, v in res.items() if "fa_mfma_fwdIDF16bLi128ELi256ELi64ELi2EDF16bLi1ELb1E" in k][0]   # persistent
+    assert c4["vgprs"] == 226 and c4["agprs"] == 0 and c4["lds_bytes"] == 65536
     assert c4["occupancy_waves_per_simd"] == 2 and c4["vgpr_spill"] == 0 and c4["scratch_bytes"] == 0
 
 
@@ -250,9 +250,10 @@ def test_theoretical_waves(vgprs, lds, threads, want):
 
 def test_candidates_name_compiled_kernels():
     res = resources_fixture()
-    # the fixture holds one fused_tuned instantiation and the d=128 fused_tc one
+    # the fixture holds one fused_tuned instantiation and the persistent d=128 fused_tc one
     assert st.find_resources(res, st.kernel_key(torch.float16, 64, 128, 32, 1, torch.float16))
-    assert st.find_resources(res, st.kernel_key(torch.bfloat16, 128, 256, 64, 2, torch.bfloat16))
+    assert st.find_resources(res, st.kernel_key(torch.bfloat16, 128, 256, 64, 2, torch.bfloat16, persistent=True))
+    assert not st.find_resources(res, st.kernel_key(torch.bfloat16, 128, 256, 64, 2, torch.bfloat16))
     assert len(st.candidates("fused_tuned", 64)) == 8
     assert st.candidates("fused_tc", 128) == [("br256_bc64_2stage", 256, 64, 2)]
 
