@@ -58,7 +58,7 @@
 //    merges them with the online-softmax rule and stores.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
-//  * PERSIST (bf16, two stages, no key split; launched only for non-causal rows whose every key
+//  * PERSIST (two stages, no key split; launched at d = 128 for non-causal rows whose every key
 //    tile is full and whose tile count is even): one workgroup per CU walks the query blocks of
 //    its XCD's range. The last two iterations of a block are separate copies of the iteration
 //    (compile-time WRAP) whose loads past the block's last tile fetch the next block's K(0),
@@ -124,8 +124,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   static_assert(L::BYTES * KSPLIT <= 65536, "K/V stages must fit ds_read's 64 KB offset reach");
   static_assert(KSPLIT == 1 || (KSPLIT == 2 && STAGES == 2 && (BM / 32) % 2 == 0),
                 "key groups: two-stage pipeline, an even number of query waves");
-  static_assert(!PERSIST || (KSPLIT == 1 && STAGES == 2 && std::is_same<T, bf16>::value),
-                "persistent form: bf16, two stages, no key split");
+  static_assert(!PERSIST || (KSPLIT == 1 && STAGES == 2), "persistent form: two stages, no key split");
 
   // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
   // cannot alias the operand reads from another, and does not make those reads wait for it.
@@ -617,30 +616,53 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 #pragma unroll
           for (int j = 0; j < 8; ++j) p_[i][j] = from_f32<T>(exp2_fast(fmaf(s_[i / 2][8 * (i % 2) + j], scale_log2, nm)));
     };
-    if (tile_of(0) < wave_tiles) {
-      qk(sa, k_stage(even));
-      if (tile_of(0) >= clean_tiles) mask(sa, tile_of(0) * BN);
-      alpha = update_max(sa, rescale);
-      exp_part(sa, pa, 0, QB, false);
-    }
+    // S(0), its row max and the first QB P registers of a block (arrays as parameters, not
+    // captures, as on the bf16 path).
+    auto first_tile = [&](f32x16 (&s0)[NKB], V8 (&p0)[PV_STEPS]) {
+      if (tile_of(0) < wave_tiles) {
+        qk(s0, k_stage(even));
+        if (!PERSIST && tile_of(0) >= clean_tiles) mask(s0, tile_of(0) * BN);
+        alpha = update_max(s0, rescale);
+        exp_part(s0, p0, 0, QB, false);
+      }
+    };
+    first_tile(sa, pa);
     // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first.
     __syncthreads();
+    // Persistent form: the next query block of this workgroup, loaded by the wrap copies (as on
+    // the bf16 path).
+    bool has_next = false;
+    int blk_n = 0;
+    auto next_base = [&]() { return (size_t)(blk_n / num_qblocks) * N * D; };
 
     // `par` is the parity of t as a compile-time constant, so every stage below is a fixed LDS
     // object: K(t+1) in k_stage(!par), V(t) in v_stage(par).
-    auto iteration = [&](auto par, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB], V8 (&pf)[PV_STEPS], V8 (&pn)[PV_STEPS]) {
+    auto iteration = [&](auto par, auto wrap, int t, f32x16 (&s)[NKB], f32x16 (&sn)[NKB], V8 (&pf)[PV_STEPS],
+                         V8 (&pn)[PV_STEPS]) {
       constexpr int P = decltype(par)::value;
+      // WRAP: the persistent form's last two iterations of a block; the loads past the block's
+      // last tile fetch the next block's K(0), K(1), V(0) and Q (as on the bf16 path).
+      constexpr bool WRAP = decltype(wrap)::value;
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
       // K(t+2) replaces K(t) (read in iteration t-1; K(0) by the first tile, before the barrier
       // above); V(t+1) replaces V(t-1) (V(1) came with the prologue). Issued first so they have
       // the whole iteration to land; waited for before its closing barrier.
       if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
-      if (t >= 1 && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
-      if (tile_of(t) < wave_tiles) {
+      else if (WRAP && has_next) load_tile(make_rsrc(K + next_base(), head_bytes), k_src, k_stage(cur), (tile_of(t + 2) - ntiles) * BN);
+      // (The persistent form also loads V(1) at t = 0: after the first block, V(1) is not in the
+      // prologue's loads. For the first block it writes the same data again.)
+      if ((PERSIST || t >= 1) && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
+      else if (WRAP && has_next && tile_of(t + 1) == ntiles) load_tile(make_rsrc(V + next_base(), head_bytes), v_src, v_stage(nxt), 0);
+      if constexpr (WRAP && P == 1) {
+        if (has_next) load_q(make_rsrc(Q + next_base(), head_bytes), (blk_n % num_qblocks) * BM + wave * 32 + lq);
+      }
+      if (PERSIST || tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
-        if (tile_of(t + 1) < clean_tiles) {
+        // Persistent form: every tile is clean, so all but the last iteration take the fast path.
+        const bool fast = PERSIST ? !(WRAP && P == 1) : (tile_of(t + 1) < clean_tiles);
+        if (fast) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/round of S(t) and,
           // if m moved, the rescale of O and l. Two copies so the common case carries no muls.
           auto phase_a = [&](auto with_rescale) {
@@ -685,7 +707,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
-            mask(sn, tile_of(t + 1) * BN);
+            if constexpr (!PERSIST) mask(sn, tile_of(t + 1) * BN);
             alpha = update_max(sn, rescale);
             exp_part(sn, pn, 0, QB, false);
           }
@@ -695,9 +717,43 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       __syncthreads();
     };
 
-    for (int t = 0; t < nit; t += 2) {
-      iteration(even, t, sa, sb, pa, pb);
-      if (t + 1 < nit) iteration(odd, t + 1, sb, sa, pb, pa);
+    const std::false_type no_wrap{};
+    if constexpr (!PERSIST) {
+      for (int t = 0; t < nit; t += 2) {
+        iteration(even, no_wrap, t, sa, sb, pa, pb);
+        if (t + 1 < nit) iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+      }
+    } else {
+      // Same launch guarantees and block walk as the bf16 path.
+      const std::true_type with_wrap{};
+      while (true) {
+        blk_n = blk + blk_step;
+        has_next = blk_n < blk_end;
+        for (int t = 0; t < nit - 2; t += 2) {
+          iteration(even, no_wrap, t, sa, sb, pa, pb);
+          iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+        }
+        iteration(even, with_wrap, nit - 2, sa, sb, pa, pb);
+        iteration(odd, with_wrap, nit - 1, sb, sa, pb, pa);
+        store_block();
+        if (!has_next) break;
+        blk = blk_n;
+        q0 = (blk % num_qblocks) * BM;
+        q0w = q0 + wave * 32;
+        qrow = q0w + lq;
+        base = (size_t)(blk / num_qblocks) * N * D;
+        q_rs = make_rsrc(Q + base, head_bytes);
+        k_rs = make_rsrc(K + base, head_bytes);
+        v_rs = make_rsrc(V + base, head_bytes);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
+        l_run = 0.f;
+        m_run = -INFINITY;
+        rescale = false;
+        alpha = 1.f;
+        first_tile(sa, pa);
+        __syncthreads();
+      }
     }
     m_out = m_run;
   } else {

@@ -85,8 +85,8 @@ int device_cus() {
   return n;
 }
 
-// The persistent bf16 d = 128 launch is on unless the environment sets PA_PERSISTENT=0 (read at
-// every launch, so a process can compare both forms).
+// The persistent d = 128 launch is on unless the environment sets PA_PERSISTENT=0 (read at every
+// launch, so a process can compare both forms).
 bool persistent_enabled() {
   const char* e = getenv("PA_PERSISTENT");
   return !(e && e[0] == '0');
@@ -98,12 +98,13 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
-  // bf16, d = 128, non-causal, N a multiple of two key tiles: the persistent form, one 8-wave
-  // workgroup per CU (its registers allow one per CU) walking the query blocks of its XCD, so the
-  // next block's first tiles load during the current block's last two. Measured on MI355X at
-  // B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024: 1184 / 1247 / 1126 / 1049
-  // against 1125 / 1198 / 1062 / 929 TFLOP/s with one workgroup per query block.
-  if constexpr (std::is_same<T, pa::bf16>::value && D == 128 && ST == 2 && KS == 1) {
+  // d = 128, non-causal, N a multiple of two key tiles: the persistent form, one 8-wave workgroup
+  // per CU (its registers allow one per CU) walking the query blocks of its XCD, so the next
+  // block's first tiles load during the current block's last two. Measured on MI355X at
+  // B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024, TFLOP/s with one workgroup per
+  // query block -> persistent: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049;
+  // fp16 1021 / 1081 / 967 / 868 -> 1043 / 1099 / 1002 / 941.
+  if constexpr (D == 128 && ST == 2 && KS == 1) {
     if (!causal && n % (2 * BN) == 0 && persistent_enabled()) {
       const long long per_xcd = (total + pa::kNumXcd - 1) / pa::kNumXcd;
       const int grid = (int)std::min<long long>(device_cus() / pa::kNumXcd, per_xcd) * pa::kNumXcd;

@@ -289,25 +289,30 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
         assert torch.equal(fn(q, k, v, causal, **kw), first)
 
 
-# The persistent bf16 d=128 launch (non-causal, N a multiple of 128: one workgroup per CU walking
+# The persistent d=128 launch (fp16 and bf16, non-causal, N a multiple of 128: one workgroup per CU walking
 # its XCD's query blocks, the next block's first tiles loaded during the current block's last two
 # iterations) runs the same arithmetic in the same order as the one-workgroup-per-block launch
 # (PA_PERSISTENT=0), so the two agree bit for bit. Shapes: 8 blocks per workgroup (C4), 2 per
 # workgroup, a block count not divisible by the 8 XCDs, fewer blocks than CUs, two key tiles per
 # row (no regular iteration between the wrap copies), N = 8192, and peaked rows that rescale
 # inside the wrap iterations.
-@pytest.mark.parametrize("shape, qk_scale, out_dtype", [
-    ((4, 32, 4096), 1.0, None),
-    ((1, 64, 2048), 1.0, torch.float32),
-    ((1, 33, 4096), 1.0, None),
-    ((1, 5, 1024), 1.0, torch.float32),
-    ((1, 304, 128), 1.0, None),
-    ((2, 16, 8192), 1.0, None),
-    ((2, 40, 1024), 10.0, torch.float32),
+@pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype", [
+    ((4, 32, 4096), torch.bfloat16, 1.0, None),
+    ((1, 64, 2048), torch.bfloat16, 1.0, torch.float32),
+    ((1, 33, 4096), torch.bfloat16, 1.0, None),
+    ((1, 5, 1024), torch.bfloat16, 1.0, torch.float32),
+    ((1, 304, 128), torch.bfloat16, 1.0, None),
+    ((2, 16, 8192), torch.bfloat16, 1.0, None),
+    ((2, 40, 1024), torch.bfloat16, 10.0, torch.float32),
+    ((4, 32, 4096), torch.float16, 1.0, None),
+    ((1, 33, 2048), torch.float16, 1.0, torch.float32),
+    ((1, 5, 1024), torch.float16, 1.0, None),
+    ((1, 304, 128), torch.float16, 1.0, torch.float32),
+    ((2, 40, 1024), torch.float16, 10.0, torch.float32),
 ])
-def test_persistent_form_matches_per_block_form(shape, qk_scale, out_dtype, monkeypatch):
-    print(f"[persistent] {shape} qk_scale={qk_scale} out={out_dtype}", flush=True)
-    q, k, v = make_qkv(*shape, 128, torch.bfloat16, seed=41, qk_scale=qk_scale, device="cuda")
+def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, monkeypatch):
+    print(f"[persistent] {shape} {dtype} qk_scale={qk_scale} out={out_dtype}", flush=True)
+    q, k, v = make_qkv(*shape, 128, dtype, seed=41, qk_scale=qk_scale, device="cuda")
     monkeypatch.delenv("PA_PERSISTENT", raising=False)
     got = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
     monkeypatch.setenv("PA_PERSISTENT", "0")
