@@ -72,7 +72,7 @@ int pa_fused_tuned_fwd(const void* q, const void* k, const void* v, void* o,
 
 /* v4 fused_tc: QK^T and PV on MFMA (fp16/bf16 in, fp32 accumulate), online softmax between.
  * dtype: F16 or BF16; out_dtype: dtype or F32; d in {64, 128}.
- * At d == 128, causal == 0 and n % 128 == 0 the launch is persistent (one workgroup per CU
+ * At d == 128, causal == 0 and an even number of 64-key tiles the launch is persistent (one workgroup per CU
  * walking the query blocks); the environment variable PA_PERSISTENT=0, read at every call,
  * selects one workgroup per query block instead. Both give the same bits.
  * Replaces attn::launch_fused_tc (csrc/kernels/fused_tc.cuh:187-196) and fused_tc_forward

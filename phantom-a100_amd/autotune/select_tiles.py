@@ -57,10 +57,10 @@ def candidates(entry: str, d: int):
 
 
 def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dtype: torch.dtype,
-               ksplit: int = 1, persistent: bool = False) -> str:
-    """Fragment of the mangled name of pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT, PERSIST>."""
+               ksplit: int = 1, persistent: bool = False, ragged: bool = False) -> str:
+    """Fragment of the mangled name of pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT, PERSIST, RAGGED>."""
     return (f"fa_mfma_fwdI{MANGLED_T[dtype]}Li{d}ELi{br}ELi{bc}ELi{stages}E{MANGLED_T[out_dtype]}"
-            f"Li{ksplit}ELb{int(persistent)}EE")
+            f"Li{ksplit}ELb{int(persistent)}ELb{int(ragged)}EE")
 
 
 def load_resources(path: str = RESOURCES) -> dict:

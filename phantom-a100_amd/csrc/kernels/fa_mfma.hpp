@@ -65,7 +65,8 @@
 //    K(1), V(0) and Q, so a block starts with its first tiles already in LDS and the per-block
 //    start-up (workgroup launch, first loads) is hidden behind the previous block. With every
 //    tile clean the mask code is compiled out and all but a block's last iteration take the
-//    fast path without a runtime test.
+//    fast path without a runtime test. RAGGED: the same walk for an even tile count whose last
+//    tile is partial; the wrap copies then take the generic path and mask that tile.
 #pragma once
 
 #include <type_traits>
@@ -97,7 +98,8 @@ template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 1
 #define PA_MFMA_OCCUPANCY
 #endif
 
-template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false>
+template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false,
+          bool RAGGED = false>
 __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT) PA_MFMA_OCCUPANCY
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
@@ -125,6 +127,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   static_assert(KSPLIT == 1 || (KSPLIT == 2 && STAGES == 2 && (BM / 32) % 2 == 0),
                 "key groups: two-stage pipeline, an even number of query waves");
   static_assert(!PERSIST || (KSPLIT == 1 && STAGES == 2), "persistent form: two stages, no key split");
+  static_assert(!RAGGED || PERSIST, "RAGGED selects the persistent form whose last key tile is partial");
 
   // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
   // cannot alias the operand reads from another, and does not make those reads wait for it.
@@ -253,6 +256,13 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   };
 
   // Mask keys past N and (causal) keys after the query.
+  // Persistent form: the wrap copies mask the same tile index in every block; an offset the
+  // compiler cannot see through keeps it from hoisting the mask's comparisons out of the block
+  // loop (~84 predicate pairs, which spill).
+  auto opaque_offset = [](int j0) __attribute__((always_inline)) {
+    if constexpr (RAGGED) asm volatile("" : "+s"(j0));
+    return j0;
+  };
   auto mask = [&](f32x16 (&s)[NKB], int j0) {
 #pragma unroll
     for (int b = 0; b < NKB; ++b)
@@ -449,11 +459,11 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       // leaving the barrier do not queue them all at once; +1.4 % on C4), otherwise here. They
       // are waited for before the iteration's closing barrier.
       // Persistent form: every tile is clean, so all but the last iteration take the fast path.
-      const bool fast = PERSIST ? kMayBeFast : (tile_of(t) < wave_tiles && tile_of(t + 1) < clean_tiles);
+      const bool fast = PERSIST ? (kMayBeFast && !(WRAP && RAGGED)) : (tile_of(t) < wave_tiles && tile_of(t + 1) < clean_tiles);
       if (!fast) {
         if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
         else if (WRAP && has_next) load_tile(make_rsrc(K + next_base(), head_bytes), k_src, k_stage(cur), (tile_of(t + 2) - ntiles) * BN);
-        if (t >= 1 && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
+        if ((PERSIST || t >= 1) && tile_of(t + 1) < ntiles) load_tile(v_rs, v_src, v_stage(nxt), tile_of(t + 1) * BN);
         else if (WRAP && has_next && tile_of(t + 1) == ntiles) load_tile(make_rsrc(V + next_base(), head_bytes), v_src, v_stage(nxt), 0);
         if constexpr (WRAP && P == 1) {
           if (has_next) load_q(make_rsrc(Q + next_base(), head_bytes), (blk_n % num_qblocks) * BM + wave * 32 + lq);
@@ -529,7 +539,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
-            if constexpr (!PERSIST) mask(sn, tile_of(t + 1) * BN);
+            if constexpr (!PERSIST || RAGGED) mask(sn, opaque_offset(tile_of(t + 1) * BN));
           }
           or_c = kTopExp;   // no P'(t+1) half was made: a fast iteration after this one recomputes
         }
@@ -661,7 +671,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
         // Persistent form: every tile is clean, so all but the last iteration take the fast path.
-        const bool fast = PERSIST ? !(WRAP && P == 1) : (tile_of(t + 1) < clean_tiles);
+        const bool fast = PERSIST ? (!(WRAP && P == 1) && !(WRAP && RAGGED)) : (tile_of(t + 1) < clean_tiles);
         if (fast) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/round of S(t) and,
           // if m moved, the rescale of O and l. Two copies so the common case carries no muls.
@@ -707,7 +717,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           pv(pf, vc);
           if (ahead) {
             qk(sn, kn);
-            if constexpr (!PERSIST) mask(sn, tile_of(t + 1) * BN);
+            if constexpr (!PERSIST || RAGGED) mask(sn, opaque_offset(tile_of(t + 1) * BN));
             alpha = update_max(sn, rescale);
             exp_part(sn, pn, 0, QB, false);
           }

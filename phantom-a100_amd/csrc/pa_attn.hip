@@ -98,21 +98,24 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
-  // d = 128, non-causal, N a multiple of two key tiles: the persistent form, one 8-wave workgroup
+  // d = 128, non-causal, an even number of key tiles: the persistent form, one 8-wave workgroup
   // per CU (its registers allow one per CU) walking the query blocks of its XCD, so the next
   // block's first tiles load during the current block's last two. Measured on MI355X at
   // B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024, TFLOP/s with one workgroup per
   // query block -> persistent: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049;
   // fp16 1021 / 1081 / 967 / 868 -> 1043 / 1099 / 1002 / 941.
   if constexpr (D == 128 && ST == 2 && KS == 1) {
-    if (!causal && n % (2 * BN) == 0 && persistent_enabled()) {
+    if (!causal && (n + BN - 1) / BN % 2 == 0 && persistent_enabled()) {
       const long long per_xcd = (total + pa::kNumXcd - 1) / pa::kNumXcd;
       const int grid = (int)std::min<long long>(device_cus() / pa::kNumXcd, per_xcd) * pa::kNumXcd;
       if (grid > 0) {
-        hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true>), dim3((unsigned)grid),
-                           dim3(BM / 32 * pa::kWave * KS), 0, stream, static_cast<const T*>(q),
-                           static_cast<const T*>(k), static_cast<const T*>(v), static_cast<OutT*>(o), n,
-                           qblocks, (int)total, scale_log2_for(D), causal);
+        // N a multiple of 2 * BN: every tile full. Otherwise (an even tile count whose last tile
+        // is partial) the RAGGED form, whose wrap copies mask that tile.
+        auto kernel = n % BN == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>
+                                  : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
+        hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
+                           static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                           static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);
         return hipGetLastError();
       }
     }

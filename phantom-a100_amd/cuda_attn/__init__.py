@@ -154,7 +154,7 @@ def fused_db(q, k, v, causal=False):
 def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False, *,
              out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """v4: both matmuls on MFMA (fp16/bf16 in, fp32 accumulate), online softmax in between.
-    FP16 or BF16, d in {64, 128}. Non-causal d=128 calls with N a multiple of 128 run the
+    FP16 or BF16, d in {64, 128}. Non-causal d=128 calls with an even number of 64-key tiles run the
     persistent launch (PA_PERSISTENT=0 in the environment selects the per-block one; same bits)."""
     _checks.check_inputs(q, k, v)
     _checks.check_tc(q, k, v)

@@ -19,9 +19,9 @@ REPO = os.path.abspath(os.path.join(HERE, "..", "..", ".."))
 PKG = os.path.join(REPO, "phantom-a100_amd")
 KERNELS = [
     "_ZN2pa13naive_softmaxEPfi",
-    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi64ELi2EfLi1ELb0EEEvPKT_S3_S3_PT4_iiifi",
-    "_ZN2pa11fa_mfma_fwdIDF16bLi128ELi256ELi64ELi2EDF16bLi1ELb1EEEvPKT_S3_S3_PT4_iiifi",
-    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi32ELi1EDF16_Li1ELb0EEEvPKT_S3_S3_PT4_iiifi",
+    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi64ELi2EfLi1ELb0ELb0EEEvPKT_S3_S3_PT4_iiifi",
+    "_ZN2pa11fa_mfma_fwdIDF16bLi128ELi256ELi64ELi2EDF16bLi1ELb1ELb0EEEvPKT_S3_S3_PT4_iiifi",
+    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi32ELi1EDF16_Li1ELb0ELb0EEEvPKT_S3_S3_PT4_iiifi",
     "_ZN2pa10fa_f32_fwdIfLi64ELi4EfEEvPKT_S3_S3_PT2_iiifi",
 ]
 

@@ -289,13 +289,13 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
         assert torch.equal(fn(q, k, v, causal, **kw), first)
 
 
-# The persistent d=128 launch (fp16 and bf16, non-causal, N a multiple of 128: one workgroup per CU walking
-# its XCD's query blocks, the next block's first tiles loaded during the current block's last two
-# iterations) runs the same arithmetic in the same order as the one-workgroup-per-block launch
-# (PA_PERSISTENT=0), so the two agree bit for bit. Shapes: 8 blocks per workgroup (C4), 2 per
-# workgroup, a block count not divisible by the 8 XCDs, fewer blocks than CUs, two key tiles per
-# row (no regular iteration between the wrap copies), N = 8192, and peaked rows that rescale
-# inside the wrap iterations.
+# The persistent d=128 launch (fp16 and bf16, non-causal, an even number of 64-key tiles: one
+# workgroup per CU walking its XCD's query blocks, the next block's first tiles loaded during the
+# current block's last two iterations) runs the same arithmetic in the same order as the
+# one-workgroup-per-block launch (PA_PERSISTENT=0), so the two agree bit for bit. Shapes: 8 blocks
+# per workgroup (C4), 2 per workgroup, a block count not divisible by the 8 XCDs, fewer blocks than
+# CUs, two key tiles per row (no regular iteration between the wrap copies), N = 8192, peaked rows
+# that rescale inside the wrap iterations, and ragged N (the RAGGED form: partial last tile).
 @pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype", [
     ((4, 32, 4096), torch.bfloat16, 1.0, None),
     ((1, 64, 2048), torch.bfloat16, 1.0, torch.float32),
@@ -309,6 +309,10 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
     ((1, 5, 1024), torch.float16, 1.0, None),
     ((1, 304, 128), torch.float16, 1.0, torch.float32),
     ((2, 40, 1024), torch.float16, 10.0, torch.float32),
+    ((2, 16, 1000), torch.bfloat16, 1.0, None),          # ragged: last tile 40 keys
+    ((1, 40, 100), torch.bfloat16, 3.0, torch.float32),  # ragged, two tiles
+    ((2, 16, 1000), torch.float16, 1.0, torch.float32),
+    ((1, 40, 100), torch.float16, 3.0, None),
 ])
 def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, monkeypatch):
     print(f"[persistent] {shape} {dtype} qk_scale={qk_scale} out={out_dtype}", flush=True)
