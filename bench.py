@@ -1,20 +1,26 @@
 """Benchmark of the attention forward path on one MI355X; prints ONE JSON line.
 
-    python bench.py                         # N=1: headline C4 + per-config table + CPU baseline
+    python bench.py                         # N=1: headline C4 + per-config table + CPU baselines
     python bench.py --steps 100 --warmup 25
     python bench.py --mode pmc              # short fixed workload for rocprofv3 --pmc runs
 
 A step is one cuda_attn.fused_tc call on the headline workload, C4: non-causal SDPA forward,
 B=4 H=32 N=4096 d=128, bf16 inputs from a seeded generator (synthetic data), already resident in
-HBM. `value` = 4*B*H*N^2*d FLOPs per step x steps / wall time of the K steps between two
-synchronisations (HIP events on the launch stream). Every config of the measurement plan is also
-timed with the reference's protocol (/root/reference/bench/benchmark.py:78-93: warm-ups, then per
-call a flush of a buffer larger than the 256 MB Infinity Cache, event timing, median/p10/p90)
-and reported under "per_config". Before timing, outputs are gated against a float64 GPU reference
+HBM. `value` = 4*B*H*N^2*d FLOPs per step x steps / the time of the K steps between two
+synchronisations (HIP events on the launch stream). MI355X raises its clock over the first ~30
+launches of this kernel, so before the warm-up a fixed-duration settle phase (--settle seconds of
+back-to-back calls, reported as `settle`) brings the clock to its steady state; the warm-up and
+the timed steps are exactly --warmup and --steps calls. Every config of the measurement plan is
+also timed with the reference's protocol (/root/reference/bench/benchmark.py:78-93: warm-ups,
+then per call a flush of a buffer larger than the 256 MB Infinity Cache, event timing,
+median/p10/p90), each after its own settle phase, and reported under "per_config" beside the
+measured device copy bandwidth. Before timing, outputs are gated against a float64 GPU reference
 on sampled heads. The CPU baseline is the oracle's NumPy restatement of the reference's online
-softmax (oracle/online_softmax.py, br=64 bc=32, P rounded to bf16) timed on a bounded sample of C4.
-"reference_workload" times fused_tc on the one shape the reference measured on hardware (A100,
-BH=324 N=128 d=64 fp16) with the reference harness's protocol and reports the ratio to its median.
+softmax (oracle/online_softmax.py, br=64 bc=32, P rounded to the config's input dtype), and
+beside it the row-chunked float64 reference, timed for every config on whole-head samples of
+the same inputs (median of 3 runs) on the host's cores. "reference_workload" times fused_tc on
+the one shape the reference measured on hardware (A100, BH=324 N=128 d=64 fp16) with the
+reference harness's protocol and reports the ratio to its median.
 """
 from __future__ import annotations
 
@@ -82,6 +88,39 @@ def time_steps(fn, steps: int, warmup: int):
     return e0.elapsed_time(e1), wall * 1e3
 
 
+def settle(fn, seconds: float) -> dict:
+    """Back-to-back calls for a fixed wall-clock duration (outside any timed region), so that the
+    clock has reached its steady state under this load before warm-up and timing."""
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        for _ in range(8):
+            fn()
+        calls += 8
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            break
+    return {"seconds": round(time.perf_counter() - t0, 3), "calls": calls}
+
+
+def copy_bandwidth(nbytes: int = 1 << 30, reps: int = 20) -> float:
+    """Device copy bandwidth in GB/s (read + write bytes / time) of a torch copy of `nbytes`:
+    the practical HBM ceiling beside the 8 TB/s specification."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+    return gbs
+
+
 def time_reference_protocol(fn, flush, warmup=10, iters=100):
     """/root/reference/bench/benchmark.py:78-93 with a flush buffer larger than the Infinity Cache."""
     for _ in range(warmup):
@@ -101,20 +140,32 @@ def time_reference_protocol(fn, flush, warmup=10, iters=100):
     return statistics.median(times), qs[0], qs[-1]
 
 
-def per_config(flush, iters: int):
+def kernel_description(cfg) -> str:
+    """The kernel instantiation and launch the library uses for cfg (its own dispatch rule)."""
+    if cfg.entry == "fused":
+        return f"fa_f32_fwd<{DTYPE_NAME[cfg.dtype]}, D=64, 4 key groups> grid {-(-cfg.N // 32) * cfg.BH} x 256 threads"
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}
+    out = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16, torch.float32: _native.DTYPE_F32}
+    return _native.fused_tc_kernel(code[cfg.dtype], out[cfg.out_dtype], cfg.BH, cfg.N, cfg.d, False)
+
+
+def per_config(flush, iters: int, settle_s: float, copy_gbs: float):
     rows = {}
     for name, cfg in CONFIGS.items():
         q, k, v = config_inputs(cfg, device="cuda")
         fn = entry_call(cfg, q, k, v)
         err = gate(cfg, q, k, v, fn)
+        st = settle(fn, settle_s)
         med, p10, p90 = time_reference_protocol(fn, flush, iters=iters)
         tf = cfg.flops() / (med * 1e-3) / 1e12
         gbs = cfg.hbm_bytes() / (med * 1e-3) / 1e9
         rows[name] = {
             "shape": [cfg.B, cfg.H, cfg.N, cfg.d], "dtype": DTYPE_NAME[cfg.dtype], "out_dtype": DTYPE_NAME[cfg.out_dtype],
-            "entry": cfg.entry, "median_ms": round(med, 5), "p10_ms": round(p10, 5), "p90_ms": round(p90, 5),
+            "entry": cfg.entry, "kernel": kernel_description(cfg), "settle": st,
+            "median_ms": round(med, 5), "p10_ms": round(p10, 5), "p90_ms": round(p90, 5),
             "tflops": round(tf, 3), "pct_mfma_peak": round(100 * tf / PEAK_TFLOPS[cfg.dtype], 3),
             "achieved_GBps": round(gbs, 1), "pct_hbm_bw": round(100 * gbs / PEAK_HBM_GBS, 3),
+            "pct_copy_bw": round(100 * gbs / copy_gbs, 3) if copy_gbs else None,
             "max_abs_err_vs_f64": float(f"{err:.3e}"),
         }
         log(f"[per-config] {name}: {med:.4f} ms  {tf:.1f} TFLOP/s  err={err:.2e}")
@@ -136,32 +187,86 @@ def reference_workload():
             "status": row["status"], "a100_median_ms": row["a100_ms"], "speedup_vs_a100": row.get("speedup_vs_a100")}
 
 
-def cpu_baseline(cfg, budget_s: float):
-    """Time the oracle's NumPy online softmax (the reference's CPU path) on whole heads of cfg."""
-    import numpy as np
-    import oracle
+def host_info() -> dict:
+    """Host CPU model, cores visible to this process and the BLAS thread count NumPy uses."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     try:
         from threadpoolctl import threadpool_info
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"cpu_model": model, "nproc": cores, "blas_threads": int(threads)}
+
+
+def _median_time(fn, runs: int):
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def cpu_baseline_config(cfg, target_s: float, runs: int = 3) -> dict:
+    """The reference's CPU path on whole heads of cfg: oracle.attention_online (br=64, bc=32,
+    P rounded to the config's input dtype; fp32 P for fp32 inputs) over as many heads as fit in
+    about `target_s` seconds per run (all heads when they fit), median of `runs` runs, scaled to
+    the whole config by heads; beside it the row-chunked float64 reference on the same heads."""
+    import numpy as np  # noqa: F401
+    import oracle
     q, k, v = (t.reshape(cfg.BH, cfg.N, cfg.d) for t in config_inputs(cfg, device="cpu"))
     p_dtype = {torch.bfloat16: "bfloat16", torch.float16: "float16"}.get(cfg.dtype)
-    heads, elapsed = 0, 0.0
-    while heads < cfg.BH and elapsed < budget_s:
-        h = heads
-        qh, kh, vh = (t[h:h + 1].float().numpy() for t in (q, k, v))
-        t0 = time.perf_counter()
-        oracle.attention_online(qh, kh, vh, False, br=64, bc=32, p_dtype=p_dtype)
-        elapsed += time.perf_counter() - t0
-        heads += 1
-    flops = 4.0 * heads * cfg.N * cfg.N * cfg.d
+
+    def sample(h):
+        return tuple(t[:h].float().numpy() for t in (q, k, v))
+
+    # size the sample from one head (one untimed call also warms the BLAS threads)
+    one = sample(1)
+    t0 = time.perf_counter()
+    oracle.attention_online(*one, False, br=64, bc=32, p_dtype=p_dtype)
+    t1 = time.perf_counter() - t0
+    heads = int(max(1, min(cfg.BH, target_s // max(t1, 1e-6))))
+    qs, ks, vs = sample(heads)
+    med, times = _median_time(lambda: oracle.attention_online(qs, ks, vs, False, br=64, bc=32, p_dtype=p_dtype), runs)
+    med64, times64 = _median_time(lambda: oracle.attention_f64_rows(qs, ks, vs, rows=512), runs)
+    scale = cfg.BH / heads
+    flops = cfg.flops()
     return {
-        "value": round(flops / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-        "sample": f"{heads} of {cfg.BH} heads of {cfg.name} (N={cfg.N}, d={cfg.d}) through "
-                  f"oracle.attention_online(br=64, bc=32, p_dtype={p_dtype}) in {elapsed:.1f} s; "
-                  f"NumPy BLAS threads={threads}, host cpus={os.cpu_count()}",
-        "seconds": round(elapsed, 2),
+        "heads": heads, "of_heads": cfg.BH, "runs": runs, "p_dtype": p_dtype or "float32",
+        "online_s_median": round(med, 4), "online_s_runs": [round(x, 4) for x in times],
+        "online_full_config_s": round(med * scale, 3), "online_tflops": round(flops / (med * scale) / 1e12, 6),
+        "f64_s_median": round(med64, 4), "f64_full_config_s": round(med64 * scale, 3),
+        "f64_tflops": round(flops / (med64 * scale) / 1e12, 6),
+    }
+
+
+def cpu_baseline(headline: str, target_s: float) -> dict:
+    """The CPU baseline of every config, reported under the bench contract's `cpu_baseline` key
+    with the headline config's attention_online rate as `value`."""
+    info = host_info()
+    rows = {}
+    for name, cfg in CONFIGS.items():
+        rows[name] = cpu_baseline_config(cfg, target_s)
+        r = rows[name]
+        log(f"[cpu] {name}: {r['heads']}/{r['of_heads']} heads, attention_online median {r['online_s_median']} s "
+            f"-> {r['online_tflops']} TFLOP/s; float64 rows {r['f64_s_median']} s")
+    h = rows[headline]
+    return {
+        "value": h["online_tflops"], "unit": "TFLOP/s", "cores": info["blas_threads"], "kind": "port",
+        "sample": (f"{h['heads']} of {h['of_heads']} heads of {headline} through oracle.attention_online(br=64, "
+                   f"bc=32, p_dtype={h['p_dtype']}), median of {h['runs']} runs, scaled to the config by heads; "
+                   f"every config under per_config; host {info['cpu_model']}, {info['nproc']} cores, "
+                   f"NumPy BLAS threads {info['blas_threads']}"),
+        **info, "per_config": rows,
     }
 
 
@@ -177,13 +282,14 @@ def traffic_from_profile():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # MI355X settles its clock under sustained MFMA load within ~25 launches of this kernel; the
-    # default warm-up covers that so the timed steps see the steady state.
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=25)
+    ap.add_argument("--settle", type=float, default=2.0,
+                    help="seconds of back-to-back calls before warm-up (clock settle; reported, not timed)")
     ap.add_argument("--config", default=HEADLINE, choices=list(CONFIGS))
     ap.add_argument("--iters", type=int, default=100, help="timed calls per config (reference protocol)")
-    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    ap.add_argument("--config-settle", type=float, default=1.0, help="settle seconds before each config's timing")
+    ap.add_argument("--cpu-target", type=float, default=3.0, help="seconds per CPU baseline run (heads sampled to fit)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-per-config", action="store_true")
     ap.add_argument("--mode", choices=["bench", "pmc"], default="bench")
@@ -223,6 +329,8 @@ def main():
         log("bench.py: correctness gate failed; not timing a wrong result")
         sys.exit(3)
 
+    st = settle(fn, args.settle)
+    log(f"[settle] {st['calls']} calls in {st['seconds']} s before warm-up")
     ms_total, wall_ms = time_steps(fn, args.steps, args.warmup)
     ms_step = ms_total / args.steps
     flops = cfg.flops()
@@ -238,12 +346,12 @@ def main():
                                f"cuda_attn.{cfg.entry}",
                    "B": cfg.B, "H": cfg.H, "N": cfg.N, "d": cfg.d, "causal": False, "entry": cfg.entry,
                    "out_dtype": DTYPE_NAME[cfg.out_dtype]},
+        "settle": dict(st, note="back-to-back calls before the warm-up, outside the timed region"),
         "roofline": {"bound": "mfma", "achieved": round(flops / (ms_step * 1e-3) / 1e12, 3),
                      "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s",
                      "frac": round(flops / (ms_step * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 5),
                      "traffic": traffic_from_profile() if cfg.name == HEADLINE else None,
-                     "kernel": "pa::fa_mfma_fwd<bf16, D=128, BM=256, BN=64, 2 stages, persistent: one workgroup per CU>",
-                     "flops_per_launch": flops},
+                     "kernel": kernel_description(cfg), "flops_per_launch": flops},
         "gate_max_abs_err": float(f"{err:.3e}"),
         "library": _native.version(),
         "device": torch.cuda.get_device_name(0),
@@ -251,13 +359,15 @@ def main():
     del q, k, v
     torch.cuda.empty_cache()
     if not args.no_per_config:
+        copy_gbs = copy_bandwidth()
+        out["copy_GBps"] = round(copy_gbs, 1)
+        log(f"[copy] device copy {copy_gbs:.0f} GB/s (read + write)")
         flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")  # > 256 MB Infinity Cache
-        out["per_config"] = per_config(flush, args.iters)
+        out["per_config"] = per_config(flush, args.iters, args.config_settle, copy_gbs)
         del flush
         out["reference_workload"] = reference_workload()
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
-        log(f"[cpu] {out['cpu_baseline']['sample']}: {out['cpu_baseline']['value']} TFLOP/s")
+        out["cpu_baseline"] = cpu_baseline(cfg.name, args.cpu_target)
     print(json.dumps(out), flush=True)
 
 

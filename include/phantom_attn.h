@@ -73,13 +73,27 @@ int pa_fused_tuned_fwd(const void* q, const void* k, const void* v, void* o,
 /* v4 fused_tc: QK^T and PV on MFMA (fp16/bf16 in, fp32 accumulate), online softmax between.
  * dtype: F16 or BF16; out_dtype: dtype or F32; d in {64, 128}.
  * At d == 128, causal == 0 and an even number of 64-key tiles the launch is persistent (one workgroup per CU
- * walking the query blocks); the environment variable PA_PERSISTENT=0, read at every call,
- * selects one workgroup per query block instead. Both give the same bits.
+ * walking the query blocks) unless pa_set_persistent(0) switched that off (see below). Both
+ * launches give the same bits.
  * Replaces attn::launch_fused_tc (csrc/kernels/fused_tc.cuh:187-196) and fused_tc_forward
  * (csrc/attn_fused_tc.cu:5-19). */
 int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o,
                     int dtype, int out_dtype, int64_t bh, int64_t n, int64_t d, int causal,
                     void* stream);
+
+/* The kernel instantiation and launch shape pa_fused_tc_fwd would use for these arguments, as
+ * text ("" if the combination is not compiled). For reports and profiles; no GPU needed (without
+ * a device the persistent launch is not chosen, as in pa_fused_tc_fwd).
+ * No reference counterpart: the reference launches one fixed kernel (csrc/kernels/fused_tc.cuh:187-196). */
+const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, int64_t d, int causal);
+
+/* Process-wide switch of fused_tc's persistent d == 128 launch: enable = 0 selects one workgroup
+ * per query block, nonzero the persistent launch. Returns the previous setting. The initial
+ * setting is read once, when the library is loaded, from the environment variable
+ * PA_PERSISTENT ("0" = off; unset or anything else = on). For A/B measurements and tests; calls
+ * already launched are not affected.
+ * No reference counterpart (the reference has one launch form). */
+int pa_set_persistent(int enable);
 
 /* LDS bytes one workgroup of fused_tuned needs, or -1 if (br, bc, d, dtype) is not compiled.
  * Replaces fused_tuned_smem_bytes (csrc/kernels/fused_tuned.cuh:188-190). No GPU needed. */

@@ -106,13 +106,18 @@ def attention_f64_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool
 
 def attention_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False,
                      br: int = 64, bc: int = 32, p_fp16: bool = False,
-                     p_dtype: str | None = None) -> np.ndarray:
+                     p_dtype: str | None = None, q_rows: tuple[int, int] | None = None) -> np.ndarray:
     """Tile-by-tile online softmax in float32, the way the fused kernels compute it.
 
     Follows /root/reference/cuda_attn/online_softmax_ref.py:27-63. ``p_fp16=True`` (or
     ``p_dtype="float16"``) rounds P to float16 before P @ V while l sums the unrounded
     float32 P; ``p_dtype="bfloat16"`` does the same with bfloat16 (extension for the
     bf16 MFMA path, which the reference does not have).
+
+    ``q_rows=(start, stop)`` computes only the query rows [start, stop) and returns them
+    (shape (..., stop - start, d)); ``start`` must be a multiple of ``br``, so every computed
+    row block is one of the full computation's (row blocks are independent: the result equals
+    those rows of the full output bit for bit). For sampling long sequences.
     """
     if p_fp16:
         if p_dtype not in (None, "float16"):
@@ -120,11 +125,14 @@ def attention_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool =
         p_dtype = "float16"
     q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
     *batch, n, d = q32.shape
-    out = np.empty_like(q32)
+    r_start, r_stop = (0, n) if q_rows is None else (int(q_rows[0]), min(int(q_rows[1]), n))
+    if r_start % br != 0 or not 0 <= r_start < r_stop:
+        raise ValueError(f"q_rows {q_rows!r}: start must be a multiple of br={br} below stop")
+    out = np.empty((*batch, r_stop - r_start, d), dtype=np.float32)
     scale_log2 = np.float32(LOG2E / np.sqrt(d))
     kt = np.swapaxes(k32, -1, -2)
 
-    for i0 in range(0, n, br):                               # one workgroup's query rows
+    for i0 in range(r_start, r_stop, br):                    # one workgroup's query rows
         i1 = min(i0 + br, n)
         qi = q32[..., i0:i1, :] * scale_log2                 # log2 domain
         r = i1 - i0
@@ -149,14 +157,15 @@ def attention_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool =
             p_mm = round_to(p, p_dtype)
             o = o * alpha[..., None] + np.matmul(p_mm, v32[..., j0:j1, :])
             m = m_new
-        out[..., i0:i1, :] = o / l[..., None]
+        res = o / l[..., None]
+        out[..., i0 - r_start:min(i1, r_stop) - r_start, :] = res[..., :min(i1, r_stop) - i0, :]
     return out
 
 
 def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False,
                            p_dtype: str | None = None, bc: int = 64, group: int = 32,
                            lazy_log2: float = 8.0, stats: dict | None = None,
-                           check: str = "max") -> np.ndarray:
+                           check: str = "max", two_term: bool = True) -> np.ndarray:
     """The fused MFMA kernel's arithmetic, in float32 (a model of this build, not the reference).
 
     Same log2-domain online softmax as ``attention_online``, with the two changes the kernel
@@ -175,12 +184,14 @@ def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: 
         fires when some rounded P' of the group reaches 2; then every row whose max grew takes
         m_ref = max + lazy_log2 - 1, O and l are multiplied by 2^(m_ref_old - m_ref_new) and
         P' is recomputed. A group's first tile always takes the exact max. m_ref starts at the
-        finite -3e38, so masked scores give P' = 0.
+        finite -3e38, so masked scores give P' = 0. With ``two_term`` (the kernel's rule), a
+        group whose rows see at most ``bc`` keys (a single tile) takes P' as two rounded terms,
+        hi = round(P') and lo = round(P' - hi), both multiplied into O and summed into l.
     ``stats``, if given, receives the largest P used (P' scaled back by 2^(lazy_log2 - 1) for
     ``"rounded"``) and the number of rescales.
     """
     if check == "rounded":
-        return _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats)
+        return _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats, two_term)
     if check != "max":
         raise ValueError(f"unknown check {check!r}")
     q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
@@ -229,7 +240,7 @@ def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: 
     return out
 
 
-def _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats):
+def _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats, two_term=True):
     """``attention_kernel_model(check="rounded")``: the bf16 kernel's overflow-check variant."""
     q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
     *batch, n, d = q32.shape
@@ -271,8 +282,18 @@ def _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats)
                 p = exp_round(m_ref)
             if p.size:
                 p_max = max(p_max, float(p.max()) * 2.0 ** float(shift))
-            l = l * alpha + p.sum(axis=-1, dtype=np.float32)
-            o = o * alpha[..., None] + np.matmul(p, v32[..., j0:j1, :])
+            terms = [p]
+            if two_term and kv_end <= bc:
+                # rows of at most bc keys (one tile): P' as hi = round(P') plus
+                # lo = round(P' - hi), both multiplied into O and summed into l (lo first)
+                with np.errstate(over="ignore"):
+                    x = np.exp2(s - m_ref[..., None]).astype(np.float32)
+                terms = [round_to((x - p).astype(np.float32), p_dtype), p]
+            l = l * alpha
+            o = o * alpha[..., None]
+            for pt in terms:
+                l = l + pt.sum(axis=-1, dtype=np.float32)
+                o = o + np.matmul(pt, v32[..., j0:j1, :])
         out[..., i0:i1, :] = o / l[..., None]
     if stats is not None:
         stats["p_max"] = p_max

@@ -23,6 +23,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import tempfile
 
@@ -33,7 +34,7 @@ sys.path.insert(0, _PKG)
 import torch  # noqa: E402
 
 import cuda_attn  # noqa: E402
-from cuda_attn import _checks  # noqa: E402
+from cuda_attn import _checks, _native  # noqa: E402
 from cuda_attn.workloads import attention_flops, compulsory_bytes  # noqa: E402
 
 from autotune import diagnose as dg  # noqa: E402
@@ -61,6 +62,21 @@ def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dt
     """Fragment of the mangled name of pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT, PERSIST, RAGGED>."""
     return (f"fa_mfma_fwdI{MANGLED_T[dtype]}Li{d}ELi{br}ELi{bc}ELi{stages}E{MANGLED_T[out_dtype]}"
             f"Li{ksplit}ELb{int(persistent)}ELb{int(ragged)}EE")
+
+
+def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal: bool, br: int) -> dict:
+    """How the library launches this call: the key split, persistent and ragged flags and the
+    number of workgroups, read from the launcher's own description (pa_fused_tc_kernel), so the
+    report names the kernel that actually runs."""
+    if entry != "fused_tc":
+        return {"ksplit": 1, "persistent": False, "ragged": False, "workgroups": -(-n // br) * bh,
+                "description": ""}
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    desc = _native.fused_tc_kernel(code, code, bh, n, d, causal)
+    grid = re.search(r"grid (\d+) x", desc)
+    return {"ksplit": 2 if "key split 2" in desc else 1, "persistent": ", persistent" in desc,
+            "ragged": ", ragged" in desc, "workgroups": int(grid.group(1)) if grid else -(-n // br) * bh,
+            "description": desc}
 
 
 def load_resources(path: str = RESOURCES) -> dict:
@@ -149,14 +165,17 @@ def evaluate(args) -> list[dict]:
             continue
         med, p10, p90 = time_calls(fn, 5, args.iters, flush)
         row.update(status="ok", median_ms=med, p10_ms=p10, p90_ms=p90, tflops=flops / (med * 1e-3) / 1e12)
-        res = find_resources(res_all, kernel_key(dt, args.dim, br, bc, st, dt))
-        threads = br // 32 * 64                  # one wave per 32 query rows
+        form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br)
+        res = find_resources(res_all, kernel_key(dt, args.dim, br, bc, st, dt, form["ksplit"], form["persistent"],
+                                                 form["ragged"]))
+        row["launch"] = form["description"]
+        threads = br // 32 * 64 * form["ksplit"]   # one wave per 32 query rows per key group
         if res:
             waves, lim = hc.theoretical_waves_per_simd(res["vgprs"], res["agprs"], res["lds_bytes"], threads)
             row.update(regs=res["vgprs"] + res["agprs"], waves_per_simd_limit=waves, occupancy_limiter=lim,
                        spill=res["vgpr_spill"] + res["sgpr_spill"] + res["scratch_bytes"])
             row["resident_wgs_per_cu"] = dg.resident_wgs_per_cu(waves, threads)
-        row["workgroups"] = -(-args.n // br) * args.batch * args.heads
+        row["workgroups"] = form["workgroups"]
         if args.profile and args.profile_dir:      # keep the raw rocprofv3 output per candidate
             prof = profile_candidate(args, br, bc, st, os.path.join(args.profile_dir, label))
         elif args.profile:

@@ -58,15 +58,15 @@
 //    merges them with the online-softmax rule and stores.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
-//  * PERSIST (two stages, no key split; launched at d = 128 for non-causal rows whose every key
-//    tile is full and whose tile count is even): one workgroup per CU walks the query blocks of
-//    its XCD's range. The last two iterations of a block are separate copies of the iteration
+//  * PERSIST (two stages, no key split; launched at d = 128 for non-causal rows whose tile count
+//    is even): one workgroup per CU walks the query blocks of its XCD's range. The last two iterations of a block are separate copies of the iteration
 //    (compile-time WRAP) whose loads past the block's last tile fetch the next block's K(0),
 //    K(1), V(0) and Q, so a block starts with its first tiles already in LDS and the per-block
-//    start-up (workgroup launch, first loads) is hidden behind the previous block. With every
-//    tile clean the mask code is compiled out and all but a block's last iteration take the
-//    fast path without a runtime test. RAGGED: the same walk for an even tile count whose last
-//    tile is partial; the wrap copies then take the generic path and mask that tile.
+//    start-up (workgroup launch, first loads) is hidden behind the previous block. When every
+//    tile is full (N a multiple of 2 * BN, RAGGED = false) the mask code is compiled out and all
+//    but a block's last iteration take the fast path without a runtime test. RAGGED: the same
+//    walk for an even tile count whose last tile is partial; both wrap iterations then take the
+//    generic path and mask that tile.
 #pragma once
 
 #include <type_traits>
@@ -458,7 +458,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       // share of both loads in every iteration: on the fast path inside phase A (so the 8 waves
       // leaving the barrier do not queue them all at once; +1.4 % on C4), otherwise here. They
       // are waited for before the iteration's closing barrier.
-      // Persistent form: every tile is clean, so all but the last iteration take the fast path.
+      // Persistent form: every tile but (RAGGED) the last is full, so every iteration outside the
+      // wrap copies takes the fast path; the last wrap copy never does, the first only when the
+      // last tile is full.
       const bool fast = PERSIST ? (kMayBeFast && !(WRAP && RAGGED)) : (tile_of(t) < wave_tiles && tile_of(t + 1) < clean_tiles);
       if (!fast) {
         if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
@@ -535,6 +537,25 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
             exact_rescale(s);
             exp_range(s, pf, c0, cf, false);
           }
+          if constexpr (!PERSIST) {
+            // Rows of at most BN keys (one tile: short causal rows, N <= BN): P' is taken as two
+            // bf16 terms, hi = round(P') (in pf) and lo = round(P' - hi) (in pn, unused without
+            // a next tile), and both go through P.V and the row sum. With few keys a single bf16
+            // P' per key (8 significant bits) leaves up to half an ulp of max|V| in O; the two
+            // terms carry ~16 bits. Longer rows average the rounding over their keys.
+            if (wave_tiles == 1) {
+              const float nm = -m_ref;
+#pragma unroll
+              for (int i = 0; i < PV_STEPS; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  const float x = exp2_fast(fmaf(s[i / 2][8 * (i % 2) + j], scale_log2, nm));
+                  pn[i][j] = from_f32<T>(x - to_f32(pf[i][j]));
+                }
+              row_sum(pn);
+              pv(pn, vc);
+            }
+          }
           row_sum(pf);
           pv(pf, vc);
           if (ahead) {
@@ -555,9 +576,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         if (t + 1 < nit) iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
       }
     } else {
-      // The launcher guarantees a non-causal launch whose N is a multiple of 2 * BN: every tile
-      // is clean and nit = ntiles is even (>= 2), so the block's last two iterations are the
-      // wrap copies and the query block is blk % num_qblocks.
+      // The launcher guarantees a non-causal launch with an even tile count nit = ntiles >= 2:
+      // the block's last two iterations are the wrap copies, only the last tile can be partial
+      // (RAGGED), and the query block is blk % num_qblocks.
       const std::true_type with_wrap{};
       while (true) {
         blk_n = blk + blk_step;
@@ -670,7 +691,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       if (PERSIST || tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
-        // Persistent form: every tile is clean, so all but the last iteration take the fast path.
+        // Persistent form: as on the bf16 path, the wrap copies of a RAGGED block take the
+        // generic path, the last wrap copy always does, every other iteration the fast path.
         const bool fast = PERSIST ? (!(WRAP && P == 1) && !(WRAP && RAGGED)) : (tile_of(t + 1) < clean_tiles);
         if (fast) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/round of S(t) and,

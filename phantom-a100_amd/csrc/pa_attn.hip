@@ -85,11 +85,28 @@ int device_cus() {
   return n;
 }
 
-// The persistent d = 128 launch is on unless the environment sets PA_PERSISTENT=0 (read at every
-// launch, so a process can compare both forms).
-bool persistent_enabled() {
+// The persistent d = 128 launch is on unless the environment sets PA_PERSISTENT=0 when the library
+// is loaded; pa_set_persistent() switches it afterwards (a process-wide flag, read once per launch).
+int persistent_from_env() {
   const char* e = getenv("PA_PERSISTENT");
-  return !(e && e[0] == '0');
+  return (e && e[0] == '0') ? 0 : 1;
+}
+std::atomic<int> g_persistent{persistent_from_env()};
+bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) != 0; }
+
+// d = 128, non-causal, an even number of key tiles: the persistent form, one 8-wave workgroup
+// per CU (its registers allow one per CU) walking the query blocks of its XCD, so the next
+// block's first tiles load during the current block's last two. Measured on MI355X at
+// B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024, TFLOP/s with one workgroup per
+// query block -> persistent: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049;
+// fp16 1021 / 1081 / 967 / 868 -> 1043 / 1099 / 1002 / 941.
+bool persistent_launch(int d, int stages, int ks, int64_t n, int bn, int causal) {
+  return d == 128 && stages == 2 && ks == 1 && !causal && (n + bn - 1) / bn % 2 == 0 && persistent_enabled();
+}
+// Workgroups of the persistent launch: one per CU, at most as many per XCD as the XCD has blocks.
+int persistent_grid(long long total_blocks) {
+  const long long per_xcd = (total_blocks + pa::kNumXcd - 1) / pa::kNumXcd;
+  return (int)std::min<long long>(device_cus() / pa::kNumXcd, per_xcd) * pa::kNumXcd;
 }
 
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1>
@@ -98,16 +115,9 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
-  // d = 128, non-causal, an even number of key tiles: the persistent form, one 8-wave workgroup
-  // per CU (its registers allow one per CU) walking the query blocks of its XCD, so the next
-  // block's first tiles load during the current block's last two. Measured on MI355X at
-  // B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024, TFLOP/s with one workgroup per
-  // query block -> persistent: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049;
-  // fp16 1021 / 1081 / 967 / 868 -> 1043 / 1099 / 1002 / 941.
   if constexpr (D == 128 && ST == 2 && KS == 1) {
-    if (!causal && (n + BN - 1) / BN % 2 == 0 && persistent_enabled()) {
-      const long long per_xcd = (total + pa::kNumXcd - 1) / pa::kNumXcd;
-      const int grid = (int)std::min<long long>(device_cus() / pa::kNumXcd, per_xcd) * pa::kNumXcd;
+    if (persistent_launch(D, ST, KS, n, BN, causal)) {
+      const int grid = persistent_grid(total);
       if (grid > 0) {
         // N a multiple of 2 * BN: every tile full. Otherwise (an even tile count whose last tile
         // is partial) the RAGGED form, whose wrap copies mask that tile.
@@ -320,6 +330,25 @@ int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o, int dt
   const MfmaEntry* e = find_tc(dtype, out_dtype, d, n, bh);
   if (!e) return fail(PA_ERR_UNSUPPORTED, "%s: output dtype must be the input dtype or float32", name);
   return hip_status(e->fn(q, k, v, o, (int)bh, (int)n, causal, static_cast<hipStream_t>(stream)), name);
+}
+
+const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, int64_t d, int causal) {
+  thread_local char desc[256];
+  const MfmaEntry* e = (bh > 0 && n > 0) ? find_tc(dtype, out_dtype, d, n, bh) : nullptr;
+  if (!e) return "";
+  static const char* dt_name[] = {"f32", "f16", "bf16"};
+  const long long total = (n + e->br - 1) / e->br * bh;
+  const int pgrid = persistent_launch(e->d, e->db ? 2 : 1, e->ks, n, e->bc, causal) ? persistent_grid(total) : 0;
+  const bool pers = pgrid > 0;   // as in launch_mfma: no device (grid 0) means one workgroup per block
+  snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s> grid %d x %d threads",
+           dt_name[e->dtype], e->d, e->br, e->bc, e->db ? 2 : 1, dt_name[e->out_dtype],
+           e->ks == 2 ? ", key split 2" : "", pers ? ", persistent" : "", pers && n % e->bc ? ", ragged" : "",
+           pers ? pgrid : (int)total, e->br / 32 * pa::kWave * e->ks);
+  return desc;
+}
+
+int pa_set_persistent(int enable) {
+  return g_persistent.exchange(enable ? 1 : 0, std::memory_order_relaxed);
 }
 
 int64_t pa_fused_tuned_lds_bytes(int br, int bc, int double_buffer, int64_t d, int dtype) {

@@ -155,7 +155,8 @@ def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = F
              out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """v4: both matmuls on MFMA (fp16/bf16 in, fp32 accumulate), online softmax in between.
     FP16 or BF16, d in {64, 128}. Non-causal d=128 calls with an even number of 64-key tiles run the
-    persistent launch (PA_PERSISTENT=0 in the environment selects the per-block one; same bits)."""
+    persistent launch (PA_PERSISTENT=0 in the environment when the library loads, or
+    cuda_attn._native.set_persistent(False), selects the per-block one; same bits)."""
     _checks.check_inputs(q, k, v)
     _checks.check_tc(q, k, v)
     od = _checks.resolve_out_dtype("fused_tc", q, out_dtype)

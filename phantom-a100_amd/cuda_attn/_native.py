@@ -28,6 +28,8 @@ PROTOTYPES = {
     "pa_fused_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i64, _i64, _i, _p]),
     "pa_fused_tuned_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i64, _i64, _i, _i, _i, _i, _p]),
     "pa_fused_tc_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i64, _i64, _i, _p]),
+    "pa_fused_tc_kernel": (ctypes.c_char_p, [_i, _i, _i64, _i64, _i64, _i]),
+    "pa_set_persistent": (_i, [_i]),
     "pa_fused_tuned_lds_bytes": (_i64, [_i, _i, _i, _i64, _i]),
     "pa_fused_tc_lds_bytes": (_i64, [_i64, _i]),
     "pa_device_lds_limit": (_i, [_i, ctypes.POINTER(_i64)]),
@@ -82,3 +84,13 @@ def device_lds_limit(device: int) -> int:
     out = ctypes.c_int64(0)
     check(lib().pa_device_lds_limit(int(device), ctypes.byref(out)), "pa_device_lds_limit")
     return int(out.value)
+
+
+def fused_tc_kernel(dtype: int, out_dtype: int, bh: int, n: int, d: int, causal: bool = False) -> str:
+    """The kernel instantiation and launch shape fused_tc would use (pa_fused_tc_kernel)."""
+    return lib().pa_fused_tc_kernel(int(dtype), int(out_dtype), int(bh), int(n), int(d), int(bool(causal))).decode()
+
+
+def set_persistent(enable: bool) -> bool:
+    """Switch fused_tc's persistent d=128 launch on or off; returns the previous setting."""
+    return bool(lib().pa_set_persistent(int(bool(enable))))

@@ -191,6 +191,25 @@ def test_native_argument_validation_without_gpu():
                       "fused_tc")
 
 
+def test_fused_tc_kernel_description_without_gpu():
+    """The launch description follows the dispatch table; with no device the persistent launch is
+    not chosen (as in pa_fused_tc_fwd), and the setter reports the previous setting."""
+    f16, bf16, f32 = _native.DTYPE_F16, _native.DTYPE_BF16, _native.DTYPE_F32
+    d128 = _native.fused_tc_kernel(bf16, bf16, 128, 4096, 128)
+    assert d128.startswith("fa_mfma_fwd<bf16, D=128, BM=256, BN=64, 2 stages, out bf16")
+    assert "grid 2048 x 512 threads" in d128
+    d64 = _native.fused_tc_kernel(f16, f32, 128, 1024, 64)
+    assert "D=64, BM=128" in d64 and "out f32" in d64 and "grid 1024 x 256 threads" in d64
+    assert "key split 2" in _native.fused_tc_kernel(f16, f16, 42, 128, 64)
+    assert _native.fused_tc_kernel(f16, f16, 1, 64, 96) == ""
+    assert _native.fused_tc_kernel(f32, f32, 1, 64, 64) == ""
+    prev = _native.set_persistent(False)
+    try:
+        assert _native.set_persistent(True) is False
+    finally:
+        _native.set_persistent(prev)
+
+
 def test_workload_accounting():
     from cuda_attn.workloads import CONFIGS
     # figures of the measurement plan: FLOPs = 4*BH*N^2*d, bytes = (3*in + out) * BH*N*d

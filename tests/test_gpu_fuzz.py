@@ -4,8 +4,10 @@ The reference's suite (tests/test_correctness.py) fixes B=2, H=4, d=64 and a lis
 draws the shape (B, H, N, d), causal, the input dtype and the output dtype per case from one fixed
 seed, within what each entry point accepts, so that shapes between the fixed ones (odd head
 counts, N just past a tile, d = 32/80 for the unfused paths, fp32 outputs) are also exercised.
-Bars: fp32 inputs 1e-4 (the reference's), fp16 2e-3, bf16 max(2e-3, 1.25 * 2^-9 * max|V|) (a few
-rounded P can carry a short causal row), each plus half an ulp of the output dtype.
+Bars: fp32 inputs 1e-4 (the reference's), fp16 2e-3, bf16 2e-3 unless the reference algorithm with
+bf16 P itself (at one of its tile configurations) misses float64 by more on the case's inputs (then the bf16 P-rounding bound
+max(2e-3, 1.25 * 2^-9 * max|V|): a few rounded P can carry a short causal row), each plus half an
+ulp of the output dtype.
 """
 from __future__ import annotations
 
@@ -17,6 +19,7 @@ import pytest
 import torch
 
 import cuda_attn
+import parity_bars as pb
 from cuda_attn.workloads import make_qkv
 
 pytestmark = pytest.mark.gpu
@@ -85,10 +88,13 @@ def test_random_shape_matches_float64(case):
     want_dtype = c["out_dtype"] or c["dtype"]
     assert out.shape == q.shape and out.dtype == want_dtype
     ref = f64_reference(q, k, v, c["causal"])
-    vmax = v.float().abs().max().item()
     bar = {torch.float32: 1e-4, torch.float16: 2e-3}.get(c["dtype"])
     if c["dtype"] == torch.bfloat16:
-        bar = max(2e-3, 1.25 * 2.0 ** -9 * vmax)
+        # 2e-3 unless the reference algorithm with bf16 P (at one of its tile configurations)
+        # misses float64 by more on these inputs
+        b, h, n, d = q.shape
+        qn, kn, vn = (t.reshape(b * h, n, d).float().cpu().numpy() for t in (q, k, v))
+        bar, _, _ = pb.reference_bar(qn, kn, vn, c["causal"], torch.bfloat16, ref.reshape(b * h, n, d).cpu().numpy())
     bar += 0.5 * torch.finfo(want_dtype).eps * ref.abs().max().item()
     err = (out.double() - ref).abs().max().item()
     assert np.isfinite(err) and err <= bar, f"{case_id(c)}: max abs error {err:.3e} > {bar:.3e}"

@@ -5,10 +5,16 @@
    scores, the N=8192 agreement check, other head dims for the unfused paths, and the
    rejection messages. Inputs come from a seeded CPU generator (same draw order as the
    reference's make_qkv) and are copied to the GPU.
-2. Golden fixtures (tests/golden): kernels against the stored float64 outputs.
+2. Golden fixtures (tests/golden): kernels against the stored float64 outputs and against the
+   reference's online softmax (oracle.attention_online, br=64 bc=32, P rounded as the kernel's
+   arithmetic rounds it) on the same inputs.
 3. The five benchmark configurations at full size, against the float64 oracle on sampled
-   heads (CPU) and a float64 GPU reference over every head; tolerance 1e-5 for fp32 inputs,
-   2e-3 for fp16/bf16 (written below per config).
+   heads (CPU), a float64 GPU reference over every head, and the reference's online softmax on
+   sampled heads and rows; tolerance 1e-5 for fp32 inputs, 2e-3 for fp16/bf16 (written below
+   per config).
+Bars for fp16/bf16 outside the configurations come from tests/parity_bars.py: 2e-3, widened to
+the P-rounding bound only where the reference algorithm itself misses float64 by more than 2e-3
+on the same inputs.
 """
 import glob
 import os
@@ -19,6 +25,7 @@ import torch
 
 import cuda_attn
 import oracle
+import parity_bars as pb
 from cuda_attn import _native
 from cuda_attn.workloads import CONFIGS, config_inputs, make_qkv
 
@@ -190,15 +197,50 @@ def test_golden(path):
         torch.cuda.synchronize()
         if dt == "float32":
             tol = 1e-5 if qk_scale == 1.0 else 1e-4
-        elif dt == "bfloat16" and causal and name == "fused_tc":
-            # bf16 P rounding on short causal rows: half a bf16 ulp of max|V| (see tests/test_oracle.py)
-            tol = max(2e-3, 2.0 ** -9 * v.float().abs().max().item() * 1.25)
+        elif name == "fused_tc":
+            # P rounded to the input dtype: 2e-3 unless the reference algorithm with the same
+            # rounding misses float64 by more on this fixture (bf16, short causal rows)
+            qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+            tol, _, _ = pb.reference_bar(qn, kn, vn, causal, dt, o.cpu().numpy())
         else:
             tol = 2e-3
         if name in ("naive", "tiled") and dt == "float16":
             tol = 2e-3 + 2.0 ** -11 * o.abs().max().item()  # fp16 output rounding
         err = max_err(out, o)
         assert err <= tol, f"{name}: max abs error {err:.3e} > {tol:.1e}"
+
+
+# Which P rounding the reference algorithm applies for an entry point: the fp32-arithmetic entry
+# points (naive, tiled, fused) keep P in fp32; the MFMA ones round P to the input dtype.
+FP32_ARITH = ("naive", "tiled", "fused")
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p)[:-4] for p in GOLDEN])
+def test_golden_matches_reference_online_softmax(path):
+    """Every entry point against the reference's own online softmax on the fixture's inputs:
+    1e-5 for fp32 inputs (1e-4 on the peaked fixture, the reference's large-score bar),
+    2e-3 for fp16/bf16 unless the reference algorithm itself misses float64 by more."""
+    q, k, v, o, causal, dt, z = load_golden(path)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    vmax = float(np.abs(vn).max())
+    qk_scale = float(z["qk_scale"])
+    for name, fn in golden_entries(dt, q.shape[-1]):
+        p_dtype = None if name in FP32_ARITH else dt
+        online = oracle.attention_online(qn, kn, vn, causal, br=64, bc=32,
+                                         p_dtype=None if p_dtype == "float32" else p_dtype)
+        if dt == "float32":
+            tol, e_ref = (1e-5 if qk_scale == 1.0 else 1e-4), None
+        elif p_dtype is None:
+            tol, e_ref = pb.BAR, None
+        else:
+            tol, e_ref, _ = pb.reference_bar(qn, kn, vn, causal, dt, o.cpu().numpy())
+        out = fn(q, k, v, causal)
+        torch.cuda.synchronize()
+        if name in ("naive", "tiled") and dt == "float16":
+            tol += 2.0 ** -11 * o.abs().max().item()  # fp16 output rounding
+        err = float(np.abs(out.float().cpu().numpy() - online).max())
+        assert err <= tol, (f"{name}: max abs error vs the reference's online softmax {err:.3e} > {tol:.1e} "
+                            f"(reference algorithm vs float64: {e_ref})")
 
 
 @pytest.mark.parametrize("path", [p for p in GOLDEN if "f16" in os.path.basename(p) or "bf16" in os.path.basename(p)],
@@ -217,11 +259,12 @@ def test_fused_tc_matches_rounded_p_model(path):
                                           v.float().cpu().numpy(), causal, p_dtype=dt, bc=64, group=32,
                                           check="rounded" if dt == "bfloat16" else "max")
     # Summation order differs (MFMA vs BLAS), so a P value close to a rounding boundary can round
-    # to the neighbouring fp16/bf16 value; one such flip moves O by at most ulp(p <= 1) * max|V| / l
-    # with l >= 1. Peaked rows (one dominant key) expose single flips; long flat rows average them.
-    ulp1 = 2.0 ** -10 if dt == "float16" else 2.0 ** -7
-    tol = max(2.5e-4, ulp1 * v.float().abs().max().item())
-    assert np.abs(out - model).max() <= tol
+    # to the neighbouring fp16/bf16 value. The bar is the one the kernel is held to against the
+    # reference algorithm (2e-3, wider only where that algorithm itself misses float64 by more).
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    tol, e_ref, _ = pb.reference_bar(qn, kn, vn, causal, dt, o.cpu().numpy())
+    err = np.abs(out - model).max()
+    assert err <= tol, f"vs the kernel model {err:.3e} > {tol:.1e} (reference algorithm vs float64: {e_ref:.2e})"
 
 
 # ---------------------------------------------------------------- 3. BASELINE configs, full size
@@ -258,6 +301,36 @@ def test_config_full_size(name):
         assert max_err(out, ref) <= tol + half_ulp
 
 
+# Query rows of each configuration checked against the reference's online softmax: whole heads at
+# N <= 1024; at N = 4096 / 8192 the first and last 512 rows (the reference algorithm is a Python
+# loop over 64 x 32 tiles, so whole heads would take minutes on the host).
+ONLINE_ROWS = {"C1": [None], "C2": [None], "C3": [None], "C4": [(0, 512), (3584, 4096)],
+               "C5": [(0, 512), (7680, 8192)]}
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_config_matches_reference_online_softmax(name):
+    """Each configuration against the reference's own computation: oracle.attention_online
+    (/root/reference/cuda_attn/online_softmax_ref.py:27-63, br=64 bc=32, P rounded to the input
+    dtype as the MFMA kernels round it; fp32 P for C1) on the same seeded inputs, sampled heads and
+    rows. Bars: 1e-5 (C1), 2e-3 (C2-C5) - the north-star bars, written here per config."""
+    cfg = CONFIGS[name]
+    tol = CONFIG_TOL[name]
+    print(f"[online {name}] shape=({cfg.B},{cfg.H},{cfg.N},{cfg.d}) dtype={cfg.dtype}", flush=True)
+    q, k, v = config_inputs(cfg, device="cuda")
+    out32 = run_config(cfg, q, k, v, torch.float32).reshape(cfg.BH, cfg.N, cfg.d)
+    heads = sorted({0, cfg.BH - 1}) if cfg.N > 1024 else sorted({0, cfg.BH // 2, cfg.BH - 1})
+    qc, kc, vc = (t.reshape(cfg.BH, cfg.N, cfg.d)[heads].float().cpu().numpy() for t in (q, k, v))
+    got = out32[heads].cpu().numpy()
+    p_dtype = pb.p_dtype_of(cfg.dtype) if cfg.entry == "fused_tc" else None
+    for rows in ONLINE_ROWS[name]:
+        online = oracle.attention_online(qc, kc, vc, False, br=64, bc=32, p_dtype=p_dtype, q_rows=rows)
+        r0, r1 = rows or (0, cfg.N)
+        err = float(np.abs(got[:, r0:r1] - online).max())
+        print(f"  rows {r0}:{r1} max abs error vs attention_online {err:.3e}", flush=True)
+        assert err <= tol, f"{name} rows {r0}:{r1}: max abs error vs attention_online {err:.3e} > {tol:.0e}"
+
+
 def test_repeat_calls_are_bitwise_identical():
     cfg = CONFIGS["C3"]
     q, k, v = config_inputs(cfg, device="cuda")
@@ -292,11 +365,13 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
 # The persistent d=128 launch (fp16 and bf16, non-causal, an even number of 64-key tiles: one
 # workgroup per CU walking its XCD's query blocks, the next block's first tiles loaded during the
 # current block's last two iterations) runs the same arithmetic in the same order as the
-# one-workgroup-per-block launch (PA_PERSISTENT=0), so the two agree bit for bit. Shapes: 8 blocks
+# one-workgroup-per-block launch (pa_set_persistent(0)), so the two agree bit for bit. Shapes: 8 blocks
 # per workgroup (C4), 2 per workgroup, a block count not divisible by the 8 XCDs, fewer blocks than
 # CUs, two key tiles per row (no regular iteration between the wrap copies), N = 8192, peaked rows
-# that rescale inside the wrap iterations, and ragged N (the RAGGED form: partial last tile).
-@pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype", [
+# that rescale inside the wrap iterations, and ragged N (the RAGGED form: partial last tile), also
+# with more query blocks than workgroups (2048 and 1024 blocks, and 600 two-tile blocks), so that
+# a workgroup loads its next block's K(0), K(1), V(0) and Q after masking its partial last tile.
+PERSISTENT_SHAPES = [
     ((4, 32, 4096), torch.bfloat16, 1.0, None),
     ((1, 64, 2048), torch.bfloat16, 1.0, torch.float32),
     ((1, 33, 4096), torch.bfloat16, 1.0, None),
@@ -313,23 +388,48 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
     ((1, 40, 100), torch.bfloat16, 3.0, torch.float32),  # ragged, two tiles
     ((2, 16, 1000), torch.float16, 1.0, torch.float32),
     ((1, 40, 100), torch.float16, 3.0, None),
-])
-def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, monkeypatch):
+    ((4, 32, 4050), torch.bfloat16, 1.0, None),          # ragged, 2048 blocks: 8 per workgroup
+    ((16, 16, 1000), torch.bfloat16, 1.0, torch.float32),  # ragged, 1024 blocks
+    ((1, 600, 100), torch.bfloat16, 3.0, None),          # ragged, two tiles, 600 blocks
+    ((4, 32, 4050), torch.float16, 1.0, torch.float32),
+    ((16, 16, 1000), torch.float16, 1.0, None),
+    ((1, 600, 100), torch.float16, 3.0, torch.float32),
+]
+
+
+@pytest.fixture
+def per_block_launch():
+    """Switch the persistent launch off for the duration of a test (restored afterwards)."""
+    prev = _native.set_persistent(True)
+    yield lambda on: _native.set_persistent(on)
+    _native.set_persistent(prev)
+
+
+@pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype", PERSISTENT_SHAPES)
+def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, per_block_launch):
+    b, h, n = shape
     print(f"[persistent] {shape} {dtype} qk_scale={qk_scale} out={out_dtype}", flush=True)
     q, k, v = make_qkv(*shape, 128, dtype, seed=41, qk_scale=qk_scale, device="cuda")
-    monkeypatch.delenv("PA_PERSISTENT", raising=False)
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    od = code if out_dtype is None else _native.DTYPE_F32
+    per_block_launch(True)
+    assert "persistent" in _native.fused_tc_kernel(code, od, b * h, n, 128)
     got = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
-    monkeypatch.setenv("PA_PERSISTENT", "0")
+    per_block_launch(False)
+    assert "persistent" not in _native.fused_tc_kernel(code, od, b * h, n, 128)
     want = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
-    b, h, n = shape
     heads = sorted({0, b * h // 2, b * h - 1})
     qh, kh, vh = (t.reshape(1, b * h, n, 128)[:, heads] for t in (q, k, v))
     ref = f64_reference_gpu(qh, kh, vh)
-    vmax = v.float().abs().max().item()
-    assert max_err(got.reshape(1, b * h, n, 128)[:, heads], ref) <= max(2e-3, 1.25 * 2.0 ** -9 * vmax) + (
-        0.5 * torch.finfo(got.dtype).eps * ref.abs().max().item())
+    rows = None if n <= 1024 else (0, 1024)
+    r0, r1 = rows or (0, n)
+    qn, kn, vn = (t[0].float().cpu().numpy() for t in (qh, kh, vh))
+    tol, e_ref, _ = pb.reference_bar(qn, kn, vn, False, dtype, ref[0, :, r0:r1].cpu().numpy(), q_rows=rows)
+    out_ulp = 0.5 * torch.finfo(got.dtype).eps * ref.abs().max().item()
+    err = max_err(got.reshape(1, b * h, n, 128)[:, heads], ref)
+    assert err <= tol + out_ulp, f"max abs error {err:.3e} > {tol:.1e} (reference algorithm vs float64 {e_ref:.2e})"
 
 
 @pytest.mark.parametrize("n", [1, 15, 63, 64, 65, 200, 1000])
@@ -339,17 +439,22 @@ def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtyp
 def test_bf16_ragged_and_peaked(n, d, causal, qk_scale):
     """The bf16 path (overflow check on the rounded P' instead of a row max) at ragged N, both head
     dims, causal, and peaked rows (Q, K x3 and x10: frequent rescales, and P' overflowing to inf
-    before the exact path takes over). Against float64 with the bf16
-    P-rounding bound (short causal rows and peaked rows put most weight on a few rounded P), and
-    against the oracle's model of the same arithmetic with the rounding-flip bound."""
+    before the exact path takes over). Against float64, against the reference algorithm with bf16
+    P and against the oracle's model of the kernel's arithmetic, each at 2e-3 unless the reference
+    algorithm itself misses float64 by more on these inputs (short causal rows and peaked rows put
+    most weight on a few rounded P); the test prints which bar applied."""
     print(f"[bf16] n={n} d={d} causal={causal} qk_scale={qk_scale}", flush=True)
     q, k, v = make_qkv(1, 3, n, d, torch.bfloat16, seed=31, qk_scale=qk_scale, device="cuda")
     out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)
-    vmax = v.float().abs().max().item()
-    assert max_err(out, f64_reference_gpu(q, k, v, causal)) <= max(2e-3, 1.25 * 2.0 ** -9 * vmax)
-    model = oracle.attention_kernel_model(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
-                                          causal, p_dtype="bfloat16", bc=64, group=32, check="rounded")
-    assert np.abs(out.cpu().numpy() - model).max() <= max(2.5e-4, 2.0 ** -7 * vmax)
+    qn, kn, vn = (t[0].float().cpu().numpy() for t in (q, k, v))
+    ref = f64_reference_gpu(q, k, v, causal)
+    tol, e_ref, online = pb.reference_bar(qn, kn, vn, causal, torch.bfloat16, ref[0].cpu().numpy())
+    print(f"  bar {tol:.2e} (reference algorithm vs float64 {e_ref:.2e})", flush=True)
+    got = out[0].cpu().numpy()
+    assert max_err(out, ref) <= tol
+    assert np.abs(got - online).max() <= tol
+    model = oracle.attention_kernel_model(qn, kn, vn, causal, p_dtype="bfloat16", bc=64, group=32, check="rounded")
+    assert np.abs(got - model).max() <= tol
 
 
 @pytest.mark.parametrize("n", [65, 128, 200, 256])
@@ -358,24 +463,33 @@ def test_bf16_ragged_and_peaked(n, d, causal, qk_scale):
 def test_key_split_matches_unsplit(n, dtype, causal):
     """d = 64 rows of 2-4 key tiles on a small grid take the key-split kernel (two key groups
     merged at the end); the same heads inside a 300-head batch take the unsplit one. Both match
-    float64, and each other to within P rounding."""
+    float64 and the reference algorithm, and each other, at 2e-3 (wider only where the reference
+    algorithm itself misses float64 by more)."""
     print(f"[key split] n={n} {dtype} causal={causal}", flush=True)
     q, k, v = make_qkv(1, 300, n, 64, dtype, seed=41, device="cuda")
     big = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)[:, :3]
     qs, ks, vs = (t[:, :3].contiguous() for t in (q, k, v))
     small = cuda_attn.fused_tc(qs, ks, vs, causal, out_dtype=torch.float32)
     ref = f64_reference_gpu(qs, ks, vs, causal)
-    vmax = vs.float().abs().max().item()
-    tol = 2e-3 if dtype == torch.float16 else max(2e-3, 1.25 * 2.0 ** -9 * vmax)
+    qn, kn, vn = (t[0].float().cpu().numpy() for t in (qs, ks, vs))
+    tol, e_ref, online = pb.reference_bar(qn, kn, vn, causal, dtype, ref[0].cpu().numpy())
     assert max_err(small, ref) <= tol and max_err(big, ref) <= tol
+    assert np.abs(small[0].cpu().numpy() - online).max() <= tol
     assert max_err(small, big) <= tol
 
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_c4_shape_causal_matches_float64(causal):
-    """Causal at the headline bf16 / d=128 shape (4 heads): the path the non-causal bench skips."""
+    """Causal at the headline bf16 / d=128 shape (4 heads): the path the non-causal bench skips.
+    Against float64 and the reference algorithm (bf16 P) at 2e-3, wider only if that algorithm
+    itself misses float64 by more (the first causal rows average over a handful of keys)."""
     q, k, v = make_qkv(1, 4, 4096, 128, torch.bfloat16, seed=21, device="cuda")
     out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)
     ref = f64_reference_gpu(q, k, v, causal)
-    tol = 2e-3 if not causal else max(2e-3, 2.0 ** -9 * v.float().abs().max().item() * 1.25)
+    qn, kn, vn = (t[0].float().cpu().numpy() for t in (q, k, v))
+    rows = (0, 512)   # the short causal rows, where P rounding weighs most
+    tol, e_ref, online = pb.reference_bar(qn, kn, vn, causal, torch.bfloat16, ref[0, :, :512].cpu().numpy(),
+                                          q_rows=rows)
+    print(f"  causal={causal}: bar {tol:.2e} (reference algorithm vs float64 {e_ref:.2e})", flush=True)
     assert max_err(out, ref) <= tol
+    assert np.abs(out[0, :, :512].cpu().numpy() - online).max() <= tol

@@ -54,6 +54,23 @@ def test_online_is_stable_for_large_scores(scale):
     np.testing.assert_allclose(out, attention_naive(q * scale, k * scale, v), atol=1e-4, rtol=1e-3)
 
 
+@pytest.mark.parametrize("rows", [(0, 64), (64, 300), (128, 200), (256, 300)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_online_row_sample_equals_full_rows(rows, causal):
+    """q_rows computes whole row blocks of the full computation, so its rows are bit-identical."""
+    rng = np.random.default_rng(7)
+    q, k, v = (rng.standard_normal((2, 300, 64)).astype(np.float32) for _ in range(3))
+    full = attention_online(q, k, v, causal, p_dtype="bfloat16")
+    part = attention_online(q, k, v, causal, p_dtype="bfloat16", q_rows=rows)
+    assert np.array_equal(part, full[:, rows[0]:rows[1]])
+
+
+def test_online_row_sample_rejects_unaligned_start():
+    q = np.zeros((1, 128, 64), np.float32)
+    with pytest.raises(ValueError, match="multiple of br"):
+        attention_online(q, q, q, q_rows=(10, 100))
+
+
 @pytest.mark.parametrize("br,bc", [(16, 16), (64, 32), (128, 64)])
 def test_tile_size_does_not_change_result(br, bc):
     rng = np.random.default_rng(1)
@@ -356,6 +373,25 @@ def test_kernel_model_rounded_check_rescales_growing_rows():
     got = oracle.attention_kernel_model(q, k, v, lazy_log2=8.0, stats=st, check="rounded", p_dtype="bfloat16")
     assert st["p_max"] < 2.0 ** 8 and st["rescales"] > 1
     assert np.abs(got - attention_naive(q, k, v)).max() < 2e-3
+
+
+@pytest.mark.parametrize("n, causal", [(15, False), (64, False), (64, True), (65, True), (200, True)])
+def test_kernel_model_two_term_p_on_single_tile_rows(n, causal):
+    """Rows of at most 64 keys take P' as two bf16 terms (hi + lo carry ~16 significant bits):
+    they then match float64 to ~2^-16 max|V| instead of half a bf16 ulp; rows of longer groups are
+    bit for bit the one-term model."""
+    rng = np.random.default_rng(n)
+    q, k, v = (oracle.round_bf16(rng.standard_normal((2, n, 64)).astype(np.float32)) for _ in range(3))
+    ref = attention_naive(q, k, v, causal)
+    two = oracle.attention_kernel_model(q, k, v, causal, p_dtype="bfloat16", check="rounded")
+    one = oracle.attention_kernel_model(q, k, v, causal, p_dtype="bfloat16", check="rounded", two_term=False)
+    single = slice(0, 64 if causal else (n if n <= 64 else 0))   # groups whose rows see <= 64 keys
+    vmax = float(np.abs(v).max())
+    assert np.abs(two[:, single] - ref[:, single]).max(initial=0) <= 2.0 ** -16 * vmax
+    rest = slice(single.stop, n)
+    assert np.array_equal(two[:, rest], one[:, rest])
+    if single.stop:
+        assert np.abs(one[:, single] - ref[:, single]).max() > 4 * np.abs(two[:, single] - ref[:, single]).max()
 
 
 def test_kernel_model_rejects_unknown_check():
