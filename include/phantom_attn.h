@@ -10,7 +10,8 @@
  *   - q, k, v, o are device pointers to contiguous [BH][N][d] arrays (the reference's
  *     (B, H, N, d) tensors viewed as [B*H][N][d], csrc/bindings.cpp:12-22). Inputs are only
  *     read; o is only written. The library never allocates or frees device memory: outputs and
- *     the score workspace of the unfused paths are allocated by the caller.
+ *     the score workspace of the unfused paths are allocated by the caller (pa_tiled_fwd_noalloc
+ *     instead uses a fixed array compiled into the library).
  *   - dtype / out_dtype take the PA_DTYPE_* codes below. out_dtype lets a caller ask for fp32
  *     output from fp16/bf16 inputs (the reference always writes o in the input dtype).
  *   - stream is a hipStream_t passed as void* (NULL = the null stream). Launches are
@@ -53,6 +54,18 @@ int pa_naive_fwd(const void* q, const void* k, const void* v, void* o, float* s,
  * (csrc/attn_tiled.cu:5-14). */
 int pa_tiled_fwd(const void* q, const void* k, const void* v, void* o, float* s,
                  int dtype, int64_t bh, int64_t n, int64_t d, int causal, void* stream);
+
+/* tiled_forward without allocation: pa_tiled_fwd with the score workspace taken from a static
+ * device array of the library instead of the caller. For callers that cannot allocate device
+ * memory (code under stream/graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Limit: B*H*N*N <= 16777216 scores (64 MiB, held by every GPU the library runs on until the
+ * process ends); larger calls return PA_ERR_UNSUPPORTED and should use pa_tiled_fwd. Calls no
+ * allocating routine. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, two host threads) race and must be serialised by the caller.
+ * No counterpart in the reference (its glue always allocates the workspace with torch,
+ * csrc/attn_tiled.cu:5-14). */
+int pa_tiled_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
+                         int dtype, int64_t bh, int64_t n, int64_t d, int causal, void* stream);
 
 /* v3 fused: online softmax with fp32 arithmetic throughout (fp32 MFMA, P kept in fp32).
  * dtype: F32 or F16; out_dtype: dtype or F32; d == 64.

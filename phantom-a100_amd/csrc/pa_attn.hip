@@ -243,14 +243,40 @@ hipError_t launch_tiled(const void* q, const void* k, const void* v, void* o, fl
   return hipGetLastError();
 }
 
-int unfused_common(const char* name, const void* q, const void* k, const void* v, void* o, const float* s, int dtype,
-                   int64_t bh, int64_t n, int64_t d) {
+int unfused_common(const char* name, const void* q, const void* k, const void* v, void* o, int dtype, int64_t bh,
+                   int64_t n, int64_t d) {
   if (int rc = check_common(name, q, k, v, o, bh, n, d)) return rc;
-  if (!s) return fail(PA_ERR_INVALID, "%s: null score workspace", name);
   if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_F16)
     return fail(PA_ERR_UNSUPPORTED, "%s: only float32 and float16 are supported", name);
   if (bh > 65535) return fail(PA_ERR_UNSUPPORTED, "%s: B*H must be at most 65535", name);
   if ((n + 3) / 4 > 65535) return fail(PA_ERR_UNSUPPORTED, "%s: N must be at most 262140", name);
+  return PA_OK;
+}
+
+// ------------------------------------------------------------------ tiled without allocation
+// Score workspace of pa_tiled_fwd_noalloc: a fixed device array instead of a caller-allocated
+// buffer. Every GPU the library runs on holds its own copy until the process ends. The tiled
+// kernels write every score before reading it, so nothing needs clearing between calls.
+constexpr int64_t kScratchFloats = 16ll << 20;   // 64 MiB: BH * N * N <= 16 Mi scores
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+// Device address of this device's `scratch`, looked up once per device (the host-side name of a
+// __device__ array is only a handle for the runtime, never a pointer to pass to a kernel).
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+
+int scratch_for_current_device(const char* name, float** out) {
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e, name);
+  if (dev < 0 || dev >= 64) return fail(PA_ERR_UNSUPPORTED, "%s: device index %d out of range", name, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)); e != hipSuccess) return hip_status(e, name);
+    if (!ptr) return fail(PA_ERR_INVALID, "%s: no device address for the scratch array", name);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<float*>(g_scratch_ptr[dev]);
   return PA_OK;
 }
 
@@ -266,7 +292,8 @@ extern "C" {
 int pa_naive_fwd(const void* q, const void* k, const void* v, void* o, float* s, int dtype, int64_t bh, int64_t n,
                  int64_t d, int causal, void* stream) {
   const char* name = "naive_forward";
-  if (int rc = unfused_common(name, q, k, v, o, s, dtype, bh, n, d)) return rc;
+  if (int rc = unfused_common(name, q, k, v, o, dtype, bh, n, d)) return rc;
+  if (!s) return fail(PA_ERR_INVALID, "%s: null score workspace", name);
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == PA_DTYPE_F32 ? launch_naive<float>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st)
                                        : launch_naive<pa::f16>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st);
@@ -276,7 +303,24 @@ int pa_naive_fwd(const void* q, const void* k, const void* v, void* o, float* s,
 int pa_tiled_fwd(const void* q, const void* k, const void* v, void* o, float* s, int dtype, int64_t bh, int64_t n,
                  int64_t d, int causal, void* stream) {
   const char* name = "tiled_forward";
-  if (int rc = unfused_common(name, q, k, v, o, s, dtype, bh, n, d)) return rc;
+  if (int rc = unfused_common(name, q, k, v, o, dtype, bh, n, d)) return rc;
+  if (!s) return fail(PA_ERR_INVALID, "%s: null score workspace", name);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == PA_DTYPE_F32 ? launch_tiled<float>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st)
+                                       : launch_tiled<pa::f16>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st);
+  return hip_status(e, name);
+}
+
+int pa_tiled_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int64_t bh, int64_t n,
+                         int64_t d, int causal, void* stream) {
+  const char* name = "tiled_forward_noalloc";
+  if (int rc = unfused_common(name, q, k, v, o, dtype, bh, n, d)) return rc;
+  if (n > kScratchFloats / bh / n)   // bh * n * n > kScratchFloats, without overflow
+    return fail(PA_ERR_UNSUPPORTED,
+                "%s: B*H*N*N = %.0f scores exceed the static scratch of %lld (use tiled_forward with a workspace)",
+                name, (double)bh * (double)n * (double)n, (long long)kScratchFloats);
+  float* s = nullptr;
+  if (int rc = scratch_for_current_device(name, &s)) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == PA_DTYPE_F32 ? launch_tiled<float>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st)
                                        : launch_tiled<pa::f16>(q, k, v, o, s, (int)bh, (int)n, (int)d, causal, st);

@@ -25,6 +25,7 @@ _i64 = ctypes.c_int64
 PROTOTYPES = {
     "pa_naive_fwd": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i, _p]),
     "pa_tiled_fwd": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i, _p]),
+    "pa_tiled_fwd_noalloc": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i, _p]),
     "pa_fused_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i64, _i64, _i, _p]),
     "pa_fused_tuned_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i64, _i64, _i, _i, _i, _i, _p]),
     "pa_fused_tc_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i64, _i64, _i, _p]),

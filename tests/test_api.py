@@ -183,6 +183,12 @@ def test_native_argument_validation_without_gpu():
     assert rc == _native.ERR_INVALID and "workspace" in _native.last_error()
     rc = lib.pa_tiled_fwd(p, p, p, p, p, _native.DTYPE_BF16, 1, 64, 64, 0, None)
     assert rc == _native.ERR_UNSUPPORTED and "float32 and float16" in _native.last_error()
+    rc = lib.pa_tiled_fwd_noalloc(p, p, p, p, _native.DTYPE_F16, 2, 4096, 64, 0, None)   # 2 x 4096^2 scores
+    assert rc == _native.ERR_UNSUPPORTED and "static scratch" in _native.last_error()
+    rc = lib.pa_tiled_fwd_noalloc(p, p, p, p, _native.DTYPE_F16, 65535, 262140, 64, 0, None)  # no overflow
+    assert rc == _native.ERR_UNSUPPORTED and "static scratch" in _native.last_error()
+    rc = lib.pa_tiled_fwd_noalloc(p, p, p, p, _native.DTYPE_BF16, 1, 64, 64, 0, None)
+    assert rc == _native.ERR_UNSUPPORTED and "float32 and float16" in _native.last_error()
     q = ctypes.c_void_p(258)  # misaligned
     rc = lib.pa_fused_tc_fwd(q, p, p, p, _native.DTYPE_F16, _native.DTYPE_F16, 1, 64, 64, 0, None)
     assert rc == _native.ERR_INVALID and "16-byte aligned" in _native.last_error()
