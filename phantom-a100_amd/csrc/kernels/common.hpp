@@ -19,6 +19,8 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWave = 64;
@@ -40,6 +42,15 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
 }
 __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// D = A * B + C on a 16x16x32 tile. Lane l holds A[l%16][8*(l/16)+j], B[8*(l/16)+j][l%16] and
+// C[4*(l/16) + r][l%16] in register r (the row sums of the fused kernels depend on this layout;
+// the GPU parity tests check them against the oracle).
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 // fp32 32x32x2: lane l holds A[l%32][l/32], B[l/32][l%32]; C as above.
 __device__ __forceinline__ f32x16 mfma32x32x2(float a, float b, f32x16 c) {
@@ -85,28 +96,6 @@ constexpr int kSchedDsRead = 0x100;
 
 // 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// acc + the sum of the 8 values of v via v_dot2 against (1, 1): the products are exact, the
-// accumulation is fp32. (Pairs are taken with a shuffle; extracting them from a bit-cast u32x4
-// miscompiled with this toolchain, reading the first dword four times.)
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float sum8(f16x8 v, float acc) {
-  const f16x2 one = {(f16)1.f, (f16)1.f};
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
-  return acc;
-}
-__device__ __forceinline__ float sum8(bf16x8 v, float acc) {
-  const bf16x2 one = {(bf16)1.f, (bf16)1.f};
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
-  return acc;
-}
 
 // Storage conversions, round to nearest even.
 template <typename T> __device__ __forceinline__ T from_f32(float x);

@@ -22,11 +22,16 @@
 //        O^T (d x queries)   += V^T . P^T      A = V^T read from LDS with ds_read_b64_tr_b16,
 //                                              B = P^T taken straight from the S^T accumulator
 //    In the 32x32 accumulator, lane l holds column l%32 (= one query) and 16 of its 32 rows
-//    (keys, or head dims); the other 16 sit in lane l^32. So a row max / row sum is a
-//    16-element in-lane reduction plus one v_permlane32_swap, the rescale of O is lane-local,
+//    (keys, or head dims); the other 16 sit in lane l^32. So a row max is a 16-element in-lane
+//    reduction plus one v_permlane32_swap, the rescale of O is lane-local,
 //    and P^T needs no LDS round trip: register r of the S^T block holds key
 //    8*(r/4) + 4*(l/32) + r%4, exactly the key that the PV MFMA's B operand expects in k-slot
 //    8*(l/32) + (r%8) once the A operand (V^T) is read in the same key order.
+//  * The row sum l of the rounded P also runs on the matrix core: one 16x16x32 MFMA per 16-key
+//    step multiplies a constant 0/1 operand by the P^T operand, which leaves every lane with the
+//    sum of its own query. It replaces 16 v_dot2 per tile, which cost 4-5 % of the kernel's
+//    time on the VALU; the extra MFMAs cost most of that back (net, measured: C3 +1.1 %,
+//    C4 +1.2 %, C5 +1.5 %).
 //  * K and V tiles of BN keys go HBM -> LDS with buffer_load ... lds (16 bytes per lane, no
 //    VGPR staging; rows past N arrive as zeros). One such load writes 1 KB of LDS contiguously,
 //    so rows are unpadded and 16-byte chunks are XOR-swizzled per row instead: the K operand
@@ -59,8 +64,8 @@
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
 //  * PERSIST (two stages, no key split; launched at d = 128 for non-causal rows whose tile count
-//    is even): one workgroup per CU walks the query blocks of its XCD's range. The last two iterations of a block are separate copies of the iteration
-//    (compile-time WRAP) whose loads past the block's last tile fetch the next block's K(0),
+//    is even): one workgroup per CU walks the query blocks of its XCD's range. The last two
+//    iterations of a block are separate copies of the iteration (compile-time WRAP) whose loads past the block's last tile fetch the next block's K(0),
 //    K(1), V(0) and Q, so a block starts with its first tiles already in LDS and the per-block
 //    start-up (workgroup launch, first loads) is hidden behind the previous block. When every
 //    tile is full (N a multiple of 2 * BN, RAGGED = false) the mask code is compiled out and all
@@ -142,7 +147,10 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // Waves are (key group g) x (query wave): group g takes the key tiles g, g + KSPLIT, ...
   const int g = KSPLIT == 1 ? 0 : (int)threadIdx.x / THREADS;
   const int tid = KSPLIT == 1 ? (int)threadIdx.x : (int)threadIdx.x % THREADS;
-  const int wave = tid / kWave;
+  // The persistent form keeps the wave index in an SGPR, so the LDS destinations of its tile
+  // loads (M0) are scalar arithmetic instead of v_readfirstlane per load (C4 +0.6 %); the
+  // per-block forms spill or lose occupancy with it.
+  const int wave = PERSIST ? __builtin_amdgcn_readfirstlane(tid / kWave) : tid / kWave;
   const int lane = tid % kWave;
   auto k_stage = [&](auto par) -> unsigned char* {
     if constexpr (decltype(par)::value) return k_lds1 + g * L::TILE_BYTES; else return k_lds0 + g * L::TILE_BYTES;
@@ -227,7 +235,17 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 
   float m_run = -INFINITY;  // running max of the log2-domain scores of row qrow
   float m_out = -INFINITY;  // the exponent reference O and l are scaled by, for the key-group merge
-  float l_run = 0.f;        // running sum over the 16 keys per 32 held by this lane
+  // Row sum on the matrix core: lacc += ONES . P^T per 16-key step (16x16x32). The P^T operand
+  // of lane l holds 8 keys of query l%32; with A[m][8g+j] = 1 iff (m/4)%2 == g%2, output rows
+  // 4g..4g+3 of column n sum both key halves of query n + 16*(g%2), so every lane ends with the
+  // sum of its own query (all 4 registers equal).
+  f32x4 lacc = {0.f, 0.f, 0.f, 0.f};
+  V8 ones;
+  {
+    const bool on = (((lane % 16) / 4) % 2) == ((lane / 16) % 2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = from_f32<T>(on ? 1.f : 0.f);
+  }
   f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
@@ -299,16 +317,15 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 #pragma unroll
       for (int r = 0; r < 16; ++r) pf[b * 2 + r / 8][r % 8] = from_f32<T>(exp2_fast(fmaf(s[b][r], scale_log2, neg_m)));
   };
-  // l += sum of the rounded P (v_dot2 against (1, 1): exact products, fp32 accumulation).
+  // l += sum of the rounded P: 16x16x32 MFMAs of the 0/1 operand by P^T (exact products, fp32
+  // accumulation).
   auto row_sum = [&](const V8 (&pf)[PV_STEPS]) {
-    float acc[2] = {0.f, 0.f};
 #pragma unroll
-    for (int ks_ = 0; ks_ < PV_STEPS; ++ks_) acc[ks_ % 2] = sum8(pf[ks_], acc[ks_ % 2]);
-    l_run += acc[0] + acc[1];
+    for (int ks_ = 0; ks_ < PV_STEPS; ++ks_) lacc = mfma16x16x32(ones, pf[ks_], lacc);
   };
 
   auto rescale_o = [&](float alpha) {
-    l_run *= alpha;
+    lacc *= alpha;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] *= alpha;
   };
@@ -330,7 +347,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 
   // O = O^T / l for the current block. Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
   auto store_block = [&]() {
-    const float l_tot = half_sum(l_run);
+    const float l_tot = lacc[0];
     const float inv = 1.f / l_tot;
     if (g == 0 && qrow < N) {
       OutT* orow = O + base + (size_t)qrow * D;
@@ -520,7 +537,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           // V operand reads (two per MFMA) run two MFMAs ahead of their use.
           __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-          for (int i = 0; i < PV_MFMAS; ++i) {
+          for (int i = 0; i < PV_MFMAS + PV_STEPS; ++i) {
             __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
             __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
             __builtin_amdgcn_sched_group_barrier(kSchedValu, VB, 0);
@@ -601,7 +618,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         v_rs = make_rsrc(V + base, head_bytes);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
-        l_run = 0.f;
+        lacc = f32x4{0.f, 0.f, 0.f, 0.f};
         m_ref = -3.0e38f;
         // K(0), K(1), V(0) and Q landed with the last iteration's wait; V(1) comes with
         // iteration 0's phase A, as for the first block.
@@ -724,7 +741,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           // V operand reads (two per MFMA) run two MFMAs ahead of their use.
           __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-          for (int i = 0; i < PV_MFMAS; ++i) {
+          for (int i = 0; i < PV_MFMAS + PV_STEPS; ++i) {
             __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
             __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
             __builtin_amdgcn_sched_group_barrier(kSchedValu, VB, 0);
@@ -779,7 +796,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         v_rs = make_rsrc(V + base, head_bytes);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
-        l_run = 0.f;
+        lacc = f32x4{0.f, 0.f, 0.f, 0.f};
         m_run = -INFINITY;
         rescale = false;
         alpha = 1.f;
@@ -825,7 +842,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 #pragma unroll
         for (int r = 0; r < 16; ++r) red_o[(db * 16 + r) * kWave + lane] = o[db][r];
       red_ml[lane] = m_out;
-      red_ml[kWave + lane] = l_run;
+      red_ml[kWave + lane] = lacc[0];
     }
     __syncthreads();
     if (g == 0) {
@@ -833,7 +850,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       const float m = fmaxf(m_out, m1);
       const float sc0 = (m_out == -INFINITY) ? 0.f : exp2_fast(m_out - m);
       const float sc1 = (m1 == -INFINITY) ? 0.f : exp2_fast(m1 - m);
-      l_run = sc0 * l_run + sc1 * l1;
+      lacc = sc0 * lacc + sc1 * l1;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
