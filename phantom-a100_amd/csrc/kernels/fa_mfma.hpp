@@ -495,9 +495,11 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the second half of P'(t) and
           // the overflow check of all of P'(t).
           // VALU instructions placed after each MFMA: the per-phase totals spread evenly, except
-          // at d = 128, where 2 and 3 measured 0.6-0.8 % faster than the even spread (3 and 4).
+          // at d = 128, where 2 and 2 measured fastest (C4, against (2, 3) +0.8 %, (3, 2) -1 %,
+          // (3, 3) -2 %, (4, x) -3 to -5 %; with the row sum on the matrix core, phase B has 20
+          // MFMAs for ~46 VALU instructions).
           constexpr int VA = D == 128 ? 2 : (HALF * 20 + 6 + QK_MFMAS - 1) / QK_MFMAS;
-          constexpr int VB = D == 128 ? 3 : (HALF * 20 + PV_STEPS * 4 + 3 + PV_MFMAS - 1) / PV_MFMAS;
+          constexpr int VB = D == 128 ? 2 : (HALF * 20 + PV_STEPS * 4 + 3 + PV_MFMAS - 1) / PV_MFMAS;
           qk(sn, kn);
           // This iteration's tile loads, issued inside phase A (unconditionally, to keep the phase
           // branch-free: past the last tile K reloads the last tile into the free stage, and at
@@ -716,7 +718,10 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           // if m moved, the rescale of O and l. Two copies so the common case carries no muls.
           auto phase_a = [&](auto with_rescale) {
             constexpr bool RS = decltype(with_rescale)::value;
-            constexpr int VA = ((PV_STEPS - QB) * 20 + (RS ? NDB * 16 + 2 : 0) + QK_MFMAS - 1) / QK_MFMAS;
+            // (the fused_tc d = 64 tile measured fastest at 4 and, in phase B, 8: C3 +0.5 %,
+            // C5 +0.6 % over the per-phase totals 5 and 11, within 1 % for 4-6 and 4-11)
+            constexpr int VA = (D == 64 && BM == 128 && BN == 64 && !RS)
+                                   ? 4 : ((PV_STEPS - QB) * 20 + (RS ? NDB * 16 + 2 : 0) + QK_MFMAS - 1) / QK_MFMAS;
             qk(sn, kn);
             if constexpr (RS) rescale_o(alpha);
             exp_part(s, pf, QB, PV_STEPS, true);
@@ -733,7 +738,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           if (rescale) phase_a(std::true_type{});
           else phase_a(std::false_type{});
           // Phase B: PV(t) MFMAs with the row sum of P(t) and the row max of S(t+1).
-          constexpr int VB = (PV_STEPS * 4 + NKB * 8 + 10 + QB * 20 + PV_MFMAS - 1) / PV_MFMAS;
+          constexpr int VB = (D == 64 && BM == 128 && BN == 64) ? 8 : (NKB * 8 + 10 + QB * 20 + PV_MFMAS - 1) / PV_MFMAS;
           pv(pf, vc);
           row_sum(pf);
           alpha = update_max(sn, rescale);
