@@ -94,30 +94,50 @@ int persistent_from_env() {
 std::atomic<int> g_persistent{persistent_from_env()};
 bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) != 0; }
 
-// d = 128, non-causal, an even number of key tiles: the persistent form, one 8-wave workgroup
-// per CU (its registers allow one per CU) walking the query blocks of its XCD, so the next
-// block's first tiles load during the current block's last two. Measured on MI355X at
-// B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024, TFLOP/s with one workgroup per
-// query block -> persistent: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049;
-// fp16 1021 / 1081 / 967 / 868 -> 1043 / 1099 / 1002 / 941.
-bool persistent_launch(int d, int stages, int ks, int64_t n, int bn, int causal) {
-  return d == 128 && stages == 2 && ks == 1 && !causal && (n + bn - 1) / bn % 2 == 0 && persistent_enabled();
+// fused_tc, non-causal, an even number of key tiles: the persistent form. As many workgroups as
+// fit on the device at once (d = 128: one 8-wave workgroup per CU; d = 64 fp16: three 4-wave
+// workgroups per CU) each walk the query blocks of their XCD, so the next block's first tiles
+// load during the current block's last two. Measured on MI355X, TFLOP/s with one workgroup per
+// query block -> persistent: B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024 at
+// d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
+// 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
+// C5 845 -> 890 (back to back), 605 -> 627 and 821 -> 859 under the flushing protocol.
+bool persistent_launch(bool tc, int stages, int ks, int64_t n, int bn, int causal) {
+  return tc && stages == 2 && ks == 1 && !causal && (n + bn - 1) / bn % 2 == 0 && persistent_enabled();
 }
-// Workgroups of the persistent launch: one per CU, at most as many per XCD as the XCD has blocks.
-int persistent_grid(long long total_blocks) {
+// Workgroups of the persistent launch: wgs_per_cu per CU, at most as many per XCD as the XCD has
+// blocks.
+int persistent_grid(long long total_blocks, int wgs_per_cu) {
   const long long per_xcd = (total_blocks + pa::kNumXcd - 1) / pa::kNumXcd;
-  return (int)std::min<long long>(device_cus() / pa::kNumXcd, per_xcd) * pa::kNumXcd;
+  return (int)std::min<long long>((long long)device_cus() / pa::kNumXcd * wgs_per_cu, per_xcd) * pa::kNumXcd;
 }
 
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1>
+// Workgroups of the persistent kernel that fit on one CU of the current device (queried once per
+// device), 0 if unknown.
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
+int persistent_wgs_per_cu() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>,
+                                                     BM / 32 * pa::kWave * KS, 0) != hipSuccess || n <= 0)
+      return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
 hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int bh, int n, int causal,
                        hipStream_t stream) {
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
-  if constexpr (D == 128 && ST == 2 && KS == 1) {
-    if (persistent_launch(D, ST, KS, n, BN, causal)) {
-      const int grid = persistent_grid(total);
+  if constexpr (TC && ST == 2 && KS == 1) {
+    if (persistent_launch(TC, ST, KS, n, BN, causal)) {
+      const int grid = persistent_grid(total, persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS>());
       if (grid > 0) {
         // N a multiple of 2 * BN: every tile full. Otherwise (an even tile count whose last tile
         // is partial) the RAGGED form, whose wrap copies mask that tile.
@@ -142,6 +162,8 @@ struct MfmaEntry {
   int dtype, out_dtype, d, br, bc, db, ks;
   mfma_fn fn;
   int64_t lds;
+  bool tc;                 // fused_tc entry: may take the persistent launch
+  int (*wgs_per_cu)();     // workgroups of its persistent kernel per CU (tc entries)
 };
 
 template <typename T> constexpr int dt_code();
@@ -149,13 +171,20 @@ template <> constexpr int dt_code<pa::f16>() { return PA_DTYPE_F16; }
 template <> constexpr int dt_code<pa::bf16>() { return PA_DTYPE_BF16; }
 template <> constexpr int dt_code<float>() { return PA_DTYPE_F32; }
 
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1>
-constexpr MfmaEntry mfma_entry() {
-  return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, KS, &launch_mfma<T, D, BM, BN, ST, OutT, KS>,
-                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS};
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool TC>
+constexpr int (*wgs_per_cu_fn())() {
+  if constexpr (TC && ST == 2 && KS == 1) return &persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS>;
+  else return nullptr;
 }
 
-#define PA_TC_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T>(), mfma_entry<T, D, BM, BN, ST, float>()
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
+constexpr MfmaEntry mfma_entry() {
+  return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, KS, &launch_mfma<T, D, BM, BN, ST, OutT, KS, TC>,
+                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS, TC, wgs_per_cu_fn<T, D, BM, BN, ST, OutT, KS, TC>()};
+}
+
+#define PA_TC_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T, 1, true>(), mfma_entry<T, D, BM, BN, ST, float, 1, true>()
+#define PA_TUNED_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T>(), mfma_entry<T, D, BM, BN, ST, float>()
 #define PA_TC_SPLIT_BOTH_OUT(T, D, BM, BN) mfma_entry<T, D, BM, BN, 2, T, 2>(), mfma_entry<T, D, BM, BN, 2, float, 2>()
 
 // fused_tc: one tile configuration per (dtype, d), chosen by measurement on MI355X. d = 128
@@ -183,7 +212,7 @@ bool use_key_split(int64_t d, int64_t n, int64_t bh) {
 }
 
 // fused_tuned: the reference's tile sweep set (fused_tuned.cuh:207) x {one, two} LDS stages.
-#define PA_TUNED(BR, BC) PA_TC_BOTH_OUT(pa::f16, 64, BR, BC, 1), PA_TC_BOTH_OUT(pa::f16, 64, BR, BC, 2)
+#define PA_TUNED(BR, BC) PA_TUNED_BOTH_OUT(pa::f16, 64, BR, BC, 1), PA_TUNED_BOTH_OUT(pa::f16, 64, BR, BC, 2)
 const MfmaEntry kTunedTable[] = {PA_TUNED(64, 32), PA_TUNED(64, 64), PA_TUNED(128, 32), PA_TUNED(128, 64)};
 
 const MfmaEntry* find_tc(int dtype, int out_dtype, int64_t d, int64_t n, int64_t bh) {
@@ -382,7 +411,8 @@ const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, 
   if (!e) return "";
   static const char* dt_name[] = {"f32", "f16", "bf16"};
   const long long total = (n + e->br - 1) / e->br * bh;
-  const int pgrid = persistent_launch(e->d, e->db ? 2 : 1, e->ks, n, e->bc, causal) ? persistent_grid(total) : 0;
+  const int pgrid = persistent_launch(e->tc, e->db ? 2 : 1, e->ks, n, e->bc, causal) && e->wgs_per_cu
+                        ? persistent_grid(total, e->wgs_per_cu()) : 0;
   const bool pers = pgrid > 0;   // as in launch_mfma: no device (grid 0) means one workgroup per block
   snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s> grid %d x %d threads",
            dt_name[e->dtype], e->d, e->br, e->bc, e->db ? 2 : 1, dt_name[e->out_dtype],

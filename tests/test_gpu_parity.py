@@ -371,7 +371,7 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
 # that rescale inside the wrap iterations, and ragged N (the RAGGED form: partial last tile), also
 # with more query blocks than workgroups (2048 and 1024 blocks, and 600 two-tile blocks), so that
 # a workgroup loads its next block's K(0), K(1), V(0) and Q after masking its partial last tile.
-PERSISTENT_SHAPES = [
+PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype; d = 128
     ((4, 32, 4096), torch.bfloat16, 1.0, None),
     ((1, 64, 2048), torch.bfloat16, 1.0, torch.float32),
     ((1, 33, 4096), torch.bfloat16, 1.0, None),
@@ -405,30 +405,45 @@ def per_block_launch():
     _native.set_persistent(prev)
 
 
-@pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype", PERSISTENT_SHAPES)
-def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, per_block_launch):
+# The same check for the d = 64 persistent launch (fp16: three 4-wave workgroups per CU, bf16:
+# two): the C3 and C5 shapes (1024 blocks on 768 / 512 workgroups, so some workgroups walk two
+# blocks and some one), ragged N, and two-tile rows on many blocks.
+PERSISTENT_SHAPES_D64 = [  # (B, H, N), dtype, qk_scale, out dtype; d = 64
+    ((8, 16, 1024), torch.float16, 1.0, None),
+    ((1, 16, 8192), torch.float16, 3.0, torch.float32),
+    ((2, 16, 1000), torch.float16, 1.0, torch.float32),
+    ((1, 300, 128), torch.float16, 1.0, None),
+    ((8, 16, 1024), torch.bfloat16, 1.0, None),
+    ((1, 200, 100), torch.bfloat16, 3.0, torch.float32),   # (fewer heads take the key split)
+    ((4, 16, 4050), torch.bfloat16, 1.0, None),
+]
+ALL_PERSISTENT = [(*c, 128) for c in PERSISTENT_SHAPES] + [(*c, 64) for c in PERSISTENT_SHAPES_D64]
+
+
+@pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype, d", ALL_PERSISTENT)
+def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, d, per_block_launch):
     b, h, n = shape
-    print(f"[persistent] {shape} {dtype} qk_scale={qk_scale} out={out_dtype}", flush=True)
-    q, k, v = make_qkv(*shape, 128, dtype, seed=41, qk_scale=qk_scale, device="cuda")
+    print(f"[persistent] {shape} d={d} {dtype} qk_scale={qk_scale} out={out_dtype}", flush=True)
+    q, k, v = make_qkv(*shape, d, dtype, seed=41, qk_scale=qk_scale, device="cuda")
     code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
     od = code if out_dtype is None else _native.DTYPE_F32
     per_block_launch(True)
-    assert "persistent" in _native.fused_tc_kernel(code, od, b * h, n, 128)
+    assert "persistent" in _native.fused_tc_kernel(code, od, b * h, n, d)
     got = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
     per_block_launch(False)
-    assert "persistent" not in _native.fused_tc_kernel(code, od, b * h, n, 128)
+    assert "persistent" not in _native.fused_tc_kernel(code, od, b * h, n, d)
     want = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     heads = sorted({0, b * h // 2, b * h - 1})
-    qh, kh, vh = (t.reshape(1, b * h, n, 128)[:, heads] for t in (q, k, v))
+    qh, kh, vh = (t.reshape(1, b * h, n, d)[:, heads] for t in (q, k, v))
     ref = f64_reference_gpu(qh, kh, vh)
     rows = None if n <= 1024 else (0, 1024)
     r0, r1 = rows or (0, n)
     qn, kn, vn = (t[0].float().cpu().numpy() for t in (qh, kh, vh))
     tol, e_ref, _ = pb.reference_bar(qn, kn, vn, False, dtype, ref[0, :, r0:r1].cpu().numpy(), q_rows=rows)
     out_ulp = 0.5 * torch.finfo(got.dtype).eps * ref.abs().max().item()
-    err = max_err(got.reshape(1, b * h, n, 128)[:, heads], ref)
+    err = max_err(got.reshape(1, b * h, n, d)[:, heads], ref)
     assert err <= tol + out_ulp, f"max abs error {err:.3e} > {tol:.1e} (reference algorithm vs float64 {e_ref:.2e})"
 
 
