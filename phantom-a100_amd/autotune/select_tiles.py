@@ -218,6 +218,10 @@ def report(args, rows, best) -> str:
             f"| {_fmt(100 * r['wait_frac'] if r.get('wait_frac') is not None else None, '.0f')} "
             f"| {'; '.join(b.split(' (')[0] for b in r.get('bottlenecks', [])) or '-'} |")
     lines.append("")
+    for r in rows:
+        if r.get("launch"):
+            lines.append(f"Launch of {r['candidate']}: `{r['launch']}`.")
+    lines.append("")
     if best:
         lines.append(f"**Chosen: {best['candidate']}** ({best['median_ms']:.4f} ms, {best['tflops']:.1f} TFLOP/s).")
         for r in rows:
