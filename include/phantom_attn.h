@@ -85,9 +85,11 @@ int pa_fused_tuned_fwd(const void* q, const void* k, const void* v, void* o,
 
 /* v4 fused_tc: QK^T and PV on MFMA (fp16/bf16 in, fp32 accumulate), online softmax between.
  * dtype: F16 or BF16; out_dtype: dtype or F32; d in {64, 128}.
- * At d == 128, causal == 0 and an even number of 64-key tiles the launch is persistent (one workgroup per CU
- * walking the query blocks) unless pa_set_persistent(0) switched that off (see below). Both
- * launches give the same bits.
+ * The launch is persistent (as many workgroups as fit on the device at once, walking the query
+ * blocks) for causal == 0 with an even number of 64-key tiles, and for causal != 0 with n a
+ * multiple of the query block (256 at d == 128, 128 at d == 64) and bh a multiple of 8, unless
+ * pa_set_persistent(0) switched that off (see below); otherwise one workgroup per query block.
+ * Both launches give the same bits.
  * Replaces attn::launch_fused_tc (csrc/kernels/fused_tc.cuh:187-196) and fused_tc_forward
  * (csrc/attn_fused_tc.cu:5-19). */
 int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o,
@@ -100,7 +102,7 @@ int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o,
  * No reference counterpart: the reference launches one fixed kernel (csrc/kernels/fused_tc.cuh:187-196). */
 const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, int64_t d, int causal);
 
-/* Process-wide switch of fused_tc's persistent d == 128 launch: enable = 0 selects one workgroup
+/* Process-wide switch of fused_tc's persistent launch: enable = 0 selects one workgroup
  * per query block, nonzero the persistent launch. Returns the previous setting. The initial
  * setting is read once, when the library is loaded, from the environment variable
  * PA_PERSISTENT ("0" = off; unset or anything else = on). For A/B measurements and tests; calls

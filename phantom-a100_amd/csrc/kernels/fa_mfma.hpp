@@ -63,15 +63,26 @@
 //    merges them with the online-softmax rule and stores.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
-//  * PERSIST (two stages, no key split; launched at d = 128 for non-causal rows whose tile count
-//    is even): one workgroup per CU walks the query blocks of its XCD's range. The last two
-//    iterations of a block are separate copies of the iteration (compile-time WRAP) whose loads past the block's last tile fetch the next block's K(0),
-//    K(1), V(0) and Q, so a block starts with its first tiles already in LDS and the per-block
-//    start-up (workgroup launch, first loads) is hidden behind the previous block. When every
-//    tile is full (N a multiple of 2 * BN, RAGGED = false) the mask code is compiled out and all
-//    but a block's last iteration take the fast path without a runtime test. RAGGED: the same
-//    walk for an even tile count whose last tile is partial; both wrap iterations then take the
-//    generic path and mask that tile.
+//  * PERSIST (two stages, no key split; launched for non-causal rows whose tile count is even):
+//    as many workgroups as fit at once walk the query blocks of their XCD's range. The last two
+//    iterations of a block are separate copies of the iteration (compile-time WRAP) whose loads
+//    past the block's last tile fetch the next block's K(0), K(1), V(0) and Q, so a block starts
+//    with its first tiles already in LDS and the per-block start-up (workgroup launch, first
+//    loads) is hidden behind the previous block. When every tile is full (N a multiple of
+//    2 * BN, RAGGED = false) the mask code is compiled out and all but a block's last iteration
+//    take the fast path without a runtime test. RAGGED: the same walk for an even tile count
+//    whose last tile is partial; both wrap iterations then take the generic path and mask that
+//    tile.
+//  * CAUSAL (the persistent form for causal rows, N a multiple of BM, B*H a multiple of 8): a
+//    block of query rows [q0, q0 + BM) sees its c = q0 / BN first key tiles unmasked in every
+//    wave, and then BM / BN diagonal tiles, of which wave w needs the first w / 2 + 1 (the last
+//    one masked). The c clean tiles run the clean persistent iterations; the diagonal tiles (with
+//    the two before them) run copies whose fast/generic/idle choice is made per wave at run time
+//    and whose fast path masks S(t+1) when t+1 is the wave's diagonal tile. Blocks are dealt to
+//    the workgroups of an XCD in rounds of whole heads (longest block first within a head), in a
+//    serpentine order: the workgroup that gets a round's c-th longest block gets the next
+//    round's c-th shortest, so every workgroup gets the same number of tiles, while the blocks
+//    running at once on an XCD share the K/V of few heads in its L2.
 #pragma once
 
 #include <type_traits>
@@ -104,7 +115,7 @@ template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 1
 #endif
 
 template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false,
-          bool RAGGED = false>
+          bool RAGGED = false, bool CAUSAL = false>
 __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT) PA_MFMA_OCCUPANCY
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
@@ -133,6 +144,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
                 "key groups: two-stage pipeline, an even number of query waves");
   static_assert(!PERSIST || (KSPLIT == 1 && STAGES == 2), "persistent form: two stages, no key split");
   static_assert(!RAGGED || PERSIST, "RAGGED selects the persistent form whose last key tile is partial");
+  static_assert(!CAUSAL || (PERSIST && !RAGGED && BM % (2 * BN) == 0), "CAUSAL selects the persistent causal form");
 
   // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
   // cannot alias the operand reads from another, and does not make those reads wait for it.
@@ -166,9 +178,23 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // Query block blk = (head, BM-query block). The persistent form walks the blocks of its XCD's
   // range (blk = x * range + c + C * j for the c-th of the C workgroups on XCD x), so that all
   // blocks of a head still run on one XCD.
+  // CAUSAL: XCD x owns the heads x, x + 8, x + 16, ...; its list holds their blocks head by head,
+  // longest (last query block) first within a head. Step j of the c-th of the C workgroups takes
+  // list entry j * C + c for even j and j * C + C - 1 - c for odd j (serpentine), -1 past the end.
   const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
-  int blk = 0, blk_step = 0, blk_end = 0;
-  if constexpr (PERSIST) {
+  int blk = 0, blk_step = 0, blk_end = 0, walk = 0;
+  auto causal_block = [&](int j) -> int {
+    const int wgs = (int)gridDim.x / kNumXcd, c = (int)blockIdx.x / kNumXcd;
+    const int entries = total_blocks / kNumXcd;   // the launcher guarantees B*H % 8 == 0
+    const int e = j * wgs + ((j & 1) ? wgs - 1 - c : c);
+    if (e >= entries) return -1;
+    const int head = (int)blockIdx.x % kNumXcd + kNumXcd * (e / num_qblocks);
+    return head * num_qblocks + (num_qblocks - 1 - e % num_qblocks);
+  };
+  if constexpr (CAUSAL) {
+    blk = causal_block(0);
+    if (blk < 0) return;   // more workgroups than blocks on this XCD
+  } else if constexpr (PERSIST) {
     const int range = (total_blocks + kNumXcd - 1) / kNumXcd;
     const int x = (int)blockIdx.x % kNumXcd;
     blk_step = (int)gridDim.x / kNumXcd;
@@ -179,7 +205,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     blk = xcd_remap(blockIdx.x, total_blocks);
   }
   int qb = blk % num_qblocks;
-  if (causal) qb = num_qblocks - 1 - qb;  // longest causal rows first
+  if (causal && !CAUSAL) qb = num_qblocks - 1 - qb;  // longest causal rows first
   int q0 = qb * BM;
   int q0w = q0 + wave * 32;
   int qrow = q0w + lq;
@@ -251,10 +277,11 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
 
   const int kv_end = causal ? min(N, q0 + BM) : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  // (CAUSAL: the block's tile counts, set again for every block of the walk.)
+  int ntiles = (kv_end + BN - 1) / BN;
   const int nit = (ntiles + KSPLIT - 1) / KSPLIT;   // iterations of every key group
   const int wave_kv_end = causal ? min(kv_end, q0w + 32) : kv_end;  // keys this wave can see
-  const int wave_tiles = (wave_kv_end + BN - 1) / BN;
+  int wave_tiles = (wave_kv_end + BN - 1) / BN;
   // Tiles [0, clean_tiles) need no mask for this wave: all keys < N and (causal) all keys at or
   // before the wave's first query.
   const int clean_tiles = causal ? min(N / BN, (q0w + 1) / BN) : N / BN;
@@ -280,6 +307,19 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   auto opaque_offset = [](int j0) __attribute__((always_inline)) {
     if constexpr (RAGGED) asm volatile("" : "+s"(j0));
     return j0;
+  };
+  // CAUSAL form: the causal mask of the wave's diagonal tile (N is a multiple of BM there, so no
+  // key is past N). Key j0 + off (off = 32 b + 8 (r / 4) + 4 hi + r % 4) is visible iff
+  // 32 b + 8 (r / 4) + r % 4 <= qrow - j0 - 4 hi; that limit is hidden from the compiler, which
+  // would otherwise hoist the 32 per-lane terms qrow - off out of the block loop (they spill).
+  auto mask_diag = [&](f32x16 (&s)[NKB], int j0) {
+    int lim = qrow - j0 - 4 * hi;
+    asm volatile("" : "+v"(lim));
+#pragma unroll
+    for (int b = 0; b < NKB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (b * 32 + (r / 4) * 8 + (r % 4) > lim) s[b][r] = -INFINITY;
   };
   auto mask = [&](f32x16 (&s)[NKB], int j0) {
 #pragma unroll
@@ -441,6 +481,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       if (tile_of(0) < wave_tiles) {
         qk(s0, k_stage(even));
         if (!PERSIST && tile_of(0) >= clean_tiles) mask(s0, tile_of(0) * BN);
+        if (CAUSAL && wave_tiles == 1) mask_diag(s0, 0);
         exact_rescale(s0);   // the first tile's exact max: m_ref set, O and l stay 0
         exp_range(s0, p0, c0, ch, false);
         uint32_t nb = 0;
@@ -465,8 +506,10 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       constexpr int P = decltype(par)::value;
       // WRAP: the persistent form's last two iterations of a block (t = nit-2, nit-1): loads past
       // the block's last tile fetch the next block's first tiles instead; the last one has no
-      // S(t+1) and therefore no fast-path copy.
-      constexpr bool WRAP = decltype(wrap)::value;
+      // S(t+1) and therefore no fast-path copy. DIAG (CAUSAL form): an iteration at or after the
+      // block's last clean tile pair, whose path is chosen per wave.
+      constexpr bool WRAP = (decltype(wrap)::value & 1) != 0;
+      constexpr bool DIAG = (decltype(wrap)::value & 2) != 0;
       constexpr bool kMayBeFast = !(WRAP && P == 1);
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
@@ -477,8 +520,13 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       // are waited for before the iteration's closing barrier.
       // Persistent form: every tile but (RAGGED) the last is full, so every iteration outside the
       // wrap copies takes the fast path; the last wrap copy never does, the first only when the
-      // last tile is full.
-      const bool fast = PERSIST ? (kMayBeFast && !(WRAP && RAGGED)) : (tile_of(t) < wave_tiles && tile_of(t + 1) < clean_tiles);
+      // last tile is full. DIAG: the fast path up to the wave's last tile (S(t+1) masked before
+      // phase B when t+1 is the wave's diagonal tile; on the last tile itself S(t+1) is computed
+      // and not used, which keeps the generic path, and its registers, out of these copies),
+      // idle after it.
+      const bool fast = DIAG ? (kMayBeFast && t < wave_tiles)
+                             : PERSIST ? (kMayBeFast && !(WRAP && RAGGED))
+                                       : (tile_of(t) < wave_tiles && tile_of(t + 1) < clean_tiles);
       if (!fast) {
         if (tile_of(t + 2) < ntiles) load_tile(k_rs, k_src, k_stage(cur), tile_of(t + 2) * BN);
         else if (WRAP && has_next) load_tile(make_rsrc(K + next_base(), head_bytes), k_src, k_stage(cur), (tile_of(t + 2) - ntiles) * BN);
@@ -488,7 +536,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           if (has_next) load_q(make_rsrc(Q + next_base(), head_bytes), (blk_n % num_qblocks) * BM + wave * 32 + lq);
         }
       }
-      if (PERSIST || tile_of(t) < wave_tiles) {
+      if ((PERSIST && !DIAG) || tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
         if (fast) {
@@ -524,9 +572,27 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
             __builtin_amdgcn_sched_group_barrier(kSchedValu, VA, 0);
           }
           __builtin_amdgcn_sched_barrier(0);
+          if constexpr (DIAG) {
+            if (t + 2 == wave_tiles) mask_diag(sn, (t + 1) * BN);
+          }
           if (check_fires(bits)) {
             exact_rescale(s);
             exp_range(s, pf, c0, cf, false);
+          }
+          if constexpr (DIAG) {
+            // A row of one tile (the generic path's two bf16 terms, below): the low terms first.
+            if (wave_tiles == 1) {
+              const float nm = -m_ref;
+#pragma unroll
+              for (int i = 0; i < PV_STEPS; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  const float x = exp2_fast(fmaf(s[i / 2][8 * (i % 2) + j], scale_log2, nm));
+                  pn[i][j] = from_f32<T>(x - to_f32(pf[i][j]));
+                }
+              row_sum(pn);
+              pv(pn, vc);
+            }
           }
           // Phase B: PV(t) MFMAs with the row sum of P'(t) and the first half of P'(t+1).
           pv(pf, vc);
@@ -595,25 +661,49 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         if (t + 1 < nit) iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
       }
     } else {
-      // The launcher guarantees a non-causal launch with an even tile count nit = ntiles >= 2:
-      // the block's last two iterations are the wrap copies, only the last tile can be partial
-      // (RAGGED), and the query block is blk % num_qblocks.
+      // The launcher guarantees an even tile count nit = ntiles >= 2 in every block: the block's
+      // last two iterations are the wrap copies. Non-causal: only the last tile can be partial
+      // (RAGGED), and the query block is blk % num_qblocks. CAUSAL: every query block is full.
       const std::true_type with_wrap{};
+      const std::integral_constant<int, 2> diag{};
+      const std::integral_constant<int, 3> diag_wrap{};
       while (true) {
-        blk_n = blk + blk_step;
-        has_next = blk_n < blk_end;
-        for (int t = 0; t < nit - 2; t += 2) {
-          iteration(even, no_wrap, t, sa, sb, pa, pb);
-          iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+        if constexpr (CAUSAL) {
+          blk_n = causal_block(walk + 1);
+          has_next = blk_n >= 0;
+          // Tiles [0, c) are clean in every wave; the per-wave copies start two tiles before c.
+          const int c = ntiles - BM / BN;
+          for (int t = 0; t < c - 2; t += 2) {
+            iteration(even, no_wrap, t, sa, sb, pa, pb);
+            iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+          }
+          for (int t = max(c - 2, 0); t < ntiles - 2; t += 2) {
+            iteration(even, diag, t, sa, sb, pa, pb);
+            iteration(odd, diag, t + 1, sb, sa, pb, pa);
+          }
+          iteration(even, diag_wrap, ntiles - 2, sa, sb, pa, pb);
+          iteration(odd, diag_wrap, ntiles - 1, sb, sa, pb, pa);
+        } else {
+          blk_n = blk + blk_step;
+          has_next = blk_n < blk_end;
+          for (int t = 0; t < nit - 2; t += 2) {
+            iteration(even, no_wrap, t, sa, sb, pa, pb);
+            iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+          }
+          iteration(even, with_wrap, nit - 2, sa, sb, pa, pb);
+          iteration(odd, with_wrap, nit - 1, sb, sa, pb, pa);
         }
-        iteration(even, with_wrap, nit - 2, sa, sb, pa, pb);
-        iteration(odd, with_wrap, nit - 1, sb, sa, pb, pa);
         store_block();
         if (!has_next) break;
+        ++walk;
         blk = blk_n;
         q0 = (blk % num_qblocks) * BM;
         q0w = q0 + wave * 32;
         qrow = q0w + lq;
+        if constexpr (CAUSAL) {
+          ntiles = (q0 + BM) / BN;
+          wave_tiles = (q0w + 32 + BN - 1) / BN;
+        }
         base = (size_t)(blk / num_qblocks) * N * D;
         q_rs = make_rsrc(Q + base, head_bytes);
         k_rs = make_rsrc(K + base, head_bytes);
@@ -672,6 +762,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       if (tile_of(0) < wave_tiles) {
         qk(s0, k_stage(even));
         if (!PERSIST && tile_of(0) >= clean_tiles) mask(s0, tile_of(0) * BN);
+        if (CAUSAL && wave_tiles == 1) mask_diag(s0, 0);
         alpha = update_max(s0, rescale);
         exp_part(s0, p0, 0, QB, false);
       }
@@ -691,8 +782,10 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
                          V8 (&pn)[PV_STEPS]) {
       constexpr int P = decltype(par)::value;
       // WRAP: the persistent form's last two iterations of a block; the loads past the block's
-      // last tile fetch the next block's K(0), K(1), V(0) and Q (as on the bf16 path).
-      constexpr bool WRAP = decltype(wrap)::value;
+      // last tile fetch the next block's K(0), K(1), V(0) and Q (as on the bf16 path). DIAG: as
+      // on the bf16 path.
+      constexpr bool WRAP = (decltype(wrap)::value & 1) != 0;
+      constexpr bool DIAG = (decltype(wrap)::value & 2) != 0;
       const std::integral_constant<int, P> cur{};
       const std::integral_constant<int, 1 - P> nxt{};
       // K(t+2) replaces K(t) (read in iteration t-1; K(0) by the first tile, before the barrier
@@ -707,12 +800,13 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       if constexpr (WRAP && P == 1) {
         if (has_next) load_q(make_rsrc(Q + next_base(), head_bytes), (blk_n % num_qblocks) * BM + wave * 32 + lq);
       }
-      if (PERSIST || tile_of(t) < wave_tiles) {
+      if ((PERSIST && !DIAG) || tile_of(t) < wave_tiles) {
         const unsigned char* kn = k_stage(nxt);
         const unsigned char* vc = v_stage(cur);
         // Persistent form: as on the bf16 path, the wrap copies of a RAGGED block take the
         // generic path, the last wrap copy always does, every other iteration the fast path.
-        const bool fast = PERSIST ? (!(WRAP && P == 1) && !(WRAP && RAGGED)) : (tile_of(t + 1) < clean_tiles);
+        const bool fast = DIAG ? (!(WRAP && P == 1) && t < wave_tiles)
+                               : PERSIST ? (!(WRAP && P == 1) && !(WRAP && RAGGED)) : (tile_of(t + 1) < clean_tiles);
         if (fast) {
           // Fast path, straight-line. Phase A: S(t+1) MFMAs with the exp2/round of S(t) and,
           // if m moved, the rescale of O and l. Two copies so the common case carries no muls.
@@ -737,6 +831,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           };
           if (rescale) phase_a(std::true_type{});
           else phase_a(std::false_type{});
+          if constexpr (DIAG) {
+            if (t + 2 == wave_tiles) mask_diag(sn, (t + 1) * BN);
+          }
           // Phase B: PV(t) MFMAs with the row sum of P(t) and the row max of S(t+1).
           constexpr int VB = (D == 64 && BM == 128 && BN == 64) ? 8 : (NKB * 8 + 10 + QB * 20 + PV_MFMAS - 1) / PV_MFMAS;
           pv(pf, vc);
@@ -778,23 +875,47 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         if (t + 1 < nit) iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
       }
     } else {
-      // Same launch guarantees and block walk as the bf16 path.
+      // Same launch guarantees, block walks and iteration copies as the bf16 path.
       const std::true_type with_wrap{};
+      const std::integral_constant<int, 2> diag{};
+      const std::integral_constant<int, 3> diag_wrap{};
       while (true) {
-        blk_n = blk + blk_step;
-        has_next = blk_n < blk_end;
-        for (int t = 0; t < nit - 2; t += 2) {
-          iteration(even, no_wrap, t, sa, sb, pa, pb);
-          iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+        if constexpr (CAUSAL) {
+          blk_n = causal_block(walk + 1);
+          has_next = blk_n >= 0;
+          // Tiles [0, c) are clean in every wave; the per-wave copies start two tiles before c.
+          const int c = ntiles - BM / BN;
+          for (int t = 0; t < c - 2; t += 2) {
+            iteration(even, no_wrap, t, sa, sb, pa, pb);
+            iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+          }
+          for (int t = max(c - 2, 0); t < ntiles - 2; t += 2) {
+            iteration(even, diag, t, sa, sb, pa, pb);
+            iteration(odd, diag, t + 1, sb, sa, pb, pa);
+          }
+          iteration(even, diag_wrap, ntiles - 2, sa, sb, pa, pb);
+          iteration(odd, diag_wrap, ntiles - 1, sb, sa, pb, pa);
+        } else {
+          blk_n = blk + blk_step;
+          has_next = blk_n < blk_end;
+          for (int t = 0; t < nit - 2; t += 2) {
+            iteration(even, no_wrap, t, sa, sb, pa, pb);
+            iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
+          }
+          iteration(even, with_wrap, nit - 2, sa, sb, pa, pb);
+          iteration(odd, with_wrap, nit - 1, sb, sa, pb, pa);
         }
-        iteration(even, with_wrap, nit - 2, sa, sb, pa, pb);
-        iteration(odd, with_wrap, nit - 1, sb, sa, pb, pa);
         store_block();
         if (!has_next) break;
+        ++walk;
         blk = blk_n;
         q0 = (blk % num_qblocks) * BM;
         q0w = q0 + wave * 32;
         qrow = q0w + lq;
+        if constexpr (CAUSAL) {
+          ntiles = (q0 + BM) / BN;
+          wave_tiles = (q0w + 32 + BN - 1) / BN;
+        }
         base = (size_t)(blk / num_qblocks) * N * D;
         q_rs = make_rsrc(Q + base, head_bytes);
         k_rs = make_rsrc(K + base, head_bytes);

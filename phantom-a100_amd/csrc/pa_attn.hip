@@ -102,8 +102,13 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
 // 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
 // C5 845 -> 890 (back to back), 605 -> 627 and 821 -> 859 under the flushing protocol.
-bool persistent_launch(bool tc, int stages, int ks, int64_t n, int bn, int causal) {
-  return tc && stages == 2 && ks == 1 && !causal && (n + bn - 1) / bn % 2 == 0 && persistent_enabled();
+// Causal rows take the CAUSAL form when every query block is full (N a multiple of BM) and every
+// XCD can own whole heads (B*H a multiple of 8): its workgroups walk their XCD's heads round by
+// round, so each gets the same number of key tiles (the per-block launch leaves CUs idle between
+// blocks of unequal length and ends with the most loaded CU).
+bool persistent_launch(bool tc, int stages, int ks, int64_t n, int bm, int bn, int64_t bh, int causal) {
+  if (!(tc && stages == 2 && ks == 1 && persistent_enabled())) return false;
+  return causal ? (n % bm == 0 && bh % pa::kNumXcd == 0) : (n + bn - 1) / bn % 2 == 0;
 }
 // Workgroups of the persistent launch: wgs_per_cu per CU, at most as many per XCD as the XCD has
 // blocks.
@@ -114,14 +119,14 @@ int persistent_grid(long long total_blocks, int wgs_per_cu) {
 
 // Workgroups of the persistent kernel that fit on one CU of the current device (queried once per
 // device), 0 if unknown.
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool CAUSAL>
 int persistent_wgs_per_cu() {
   static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false, CAUSAL>,
                                                      BM / 32 * pa::kWave * KS, 0) != hipSuccess || n <= 0)
       return 0;
     cache[dev].store(n, std::memory_order_relaxed);
@@ -136,13 +141,15 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
   if constexpr (TC && ST == 2 && KS == 1) {
-    if (persistent_launch(TC, ST, KS, n, BN, causal)) {
-      const int grid = persistent_grid(total, persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS>());
+    if (persistent_launch(TC, ST, KS, n, BM, BN, bh, causal)) {
+      const int grid = persistent_grid(total, causal ? persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true>()
+                                                     : persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false>());
       if (grid > 0) {
-        // N a multiple of 2 * BN: every tile full. Otherwise (an even tile count whose last tile
-        // is partial) the RAGGED form, whose wrap copies mask that tile.
-        auto kernel = n % BN == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>
-                                  : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
+        // Non-causal with N a multiple of 2 * BN: every tile full. Otherwise (an even tile count
+        // whose last tile is partial) the RAGGED form, whose wrap copies mask that tile.
+        auto kernel = causal ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false, true>
+                      : n % BN == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>
+                                    : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
         hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                            static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);
@@ -164,6 +171,7 @@ struct MfmaEntry {
   int64_t lds;
   bool tc;                 // fused_tc entry: may take the persistent launch
   int (*wgs_per_cu)();     // workgroups of its persistent kernel per CU (tc entries)
+  int (*wgs_per_cu_causal)();   // the same for its CAUSAL form
 };
 
 template <typename T> constexpr int dt_code();
@@ -171,16 +179,17 @@ template <> constexpr int dt_code<pa::f16>() { return PA_DTYPE_F16; }
 template <> constexpr int dt_code<pa::bf16>() { return PA_DTYPE_BF16; }
 template <> constexpr int dt_code<float>() { return PA_DTYPE_F32; }
 
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool TC>
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool TC, bool CAUSAL>
 constexpr int (*wgs_per_cu_fn())() {
-  if constexpr (TC && ST == 2 && KS == 1) return &persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS>;
+  if constexpr (TC && ST == 2 && KS == 1) return &persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, CAUSAL>;
   else return nullptr;
 }
 
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
 constexpr MfmaEntry mfma_entry() {
   return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, KS, &launch_mfma<T, D, BM, BN, ST, OutT, KS, TC>,
-                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS, TC, wgs_per_cu_fn<T, D, BM, BN, ST, OutT, KS, TC>()};
+                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS, TC, wgs_per_cu_fn<T, D, BM, BN, ST, OutT, KS, TC, false>(),
+                   wgs_per_cu_fn<T, D, BM, BN, ST, OutT, KS, TC, true>()};
 }
 
 #define PA_TC_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T, 1, true>(), mfma_entry<T, D, BM, BN, ST, float, 1, true>()
@@ -411,12 +420,14 @@ const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, 
   if (!e) return "";
   static const char* dt_name[] = {"f32", "f16", "bf16"};
   const long long total = (n + e->br - 1) / e->br * bh;
-  const int pgrid = persistent_launch(e->tc, e->db ? 2 : 1, e->ks, n, e->bc, causal) && e->wgs_per_cu
-                        ? persistent_grid(total, e->wgs_per_cu()) : 0;
+  int (*wgs)() = causal ? e->wgs_per_cu_causal : e->wgs_per_cu;
+  const int pgrid = persistent_launch(e->tc, e->db ? 2 : 1, e->ks, n, e->br, e->bc, bh, causal) && wgs
+                        ? persistent_grid(total, wgs()) : 0;
   const bool pers = pgrid > 0;   // as in launch_mfma: no device (grid 0) means one workgroup per block
   snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s> grid %d x %d threads",
            dt_name[e->dtype], e->d, e->br, e->bc, e->db ? 2 : 1, dt_name[e->out_dtype],
-           e->ks == 2 ? ", key split 2" : "", pers ? ", persistent" : "", pers && n % e->bc ? ", ragged" : "",
+           e->ks == 2 ? ", key split 2" : "", pers ? ", persistent" : "",
+           !pers ? "" : causal ? ", causal" : n % e->bc ? ", ragged" : "",
            pers ? pgrid : (int)total, e->br / 32 * pa::kWave * e->ks);
   return desc;
 }

@@ -447,6 +447,53 @@ def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtyp
     assert err <= tol + out_ulp, f"max abs error {err:.3e} > {tol:.1e} (reference algorithm vs float64 {e_ref:.2e})"
 
 
+# The causal persistent form (N a multiple of the block's 256 / 128 queries, B*H a multiple of 8)
+# against the per-block launch, bit for bit: C4 and C3/C5 shapes made causal, one block per head
+# (every wave's only tiles are diagonal, two-term bf16 P on one-tile rows), a block count per head
+# that is not a power of two, rescaling rows, more blocks than workgroups, fp32 outputs.
+CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
+    ((4, 32, 4096), torch.bfloat16, 1.0, None, 128),
+    ((4, 32, 4096), torch.float16, 1.0, None, 128),
+    ((2, 16, 8192), torch.bfloat16, 1.0, torch.float32, 128),
+    ((1, 8, 256), torch.bfloat16, 1.0, torch.float32, 128),
+    ((1, 16, 768), torch.bfloat16, 10.0, torch.float32, 128),
+    ((2, 8, 1024), torch.float16, 3.0, torch.float32, 128),
+    ((4, 64, 1024), torch.bfloat16, 1.0, None, 128),
+    ((8, 16, 1024), torch.float16, 1.0, None, 64),
+    ((1, 16, 8192), torch.float16, 3.0, torch.float32, 64),
+    ((4, 64, 128), torch.bfloat16, 1.0, torch.float32, 64),
+    ((2, 8, 384), torch.bfloat16, 3.0, None, 64),
+    ((2, 8, 640), torch.float16, 10.0, torch.float32, 64),
+]
+
+
+@pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype, d", CAUSAL_PERSISTENT_SHAPES)
+def test_causal_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, d, per_block_launch):
+    b, h, n = shape
+    print(f"[causal persistent] {shape} d={d} {dtype} qk_scale={qk_scale} out={out_dtype}", flush=True)
+    q, k, v = make_qkv(*shape, d, dtype, seed=43, qk_scale=qk_scale, device="cuda")
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    od = code if out_dtype is None else _native.DTYPE_F32
+    per_block_launch(True)
+    assert "persistent, causal" in _native.fused_tc_kernel(code, od, b * h, n, d, True)
+    got = cuda_attn.fused_tc(q, k, v, True, out_dtype=out_dtype)
+    per_block_launch(False)
+    assert "persistent" not in _native.fused_tc_kernel(code, od, b * h, n, d, True)
+    want = cuda_attn.fused_tc(q, k, v, True, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    heads = sorted({0, b * h // 2, b * h - 1})
+    qh, kh, vh = (t.reshape(1, b * h, n, d)[:, heads] for t in (q, k, v))
+    ref = f64_reference_gpu(qh, kh, vh, causal=True)
+    rows = None if n <= 1024 else (0, 1024)
+    r0, r1 = rows or (0, n)
+    qn, kn, vn = (t[0].float().cpu().numpy() for t in (qh, kh, vh))
+    tol, e_ref, _ = pb.reference_bar(qn, kn, vn, True, dtype, ref[0, :, r0:r1].cpu().numpy(), q_rows=rows)
+    out_ulp = 0.5 * torch.finfo(got.dtype).eps * ref.abs().max().item()
+    err = max_err(got.reshape(1, b * h, n, d)[:, heads], ref)
+    assert err <= tol + out_ulp, f"max abs error {err:.3e} > {tol:.1e} (reference algorithm vs float64 {e_ref:.2e})"
+
+
 @pytest.mark.parametrize("n", [1, 15, 63, 64, 65, 200, 1000])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
