@@ -58,10 +58,11 @@ def candidates(entry: str, d: int):
 
 
 def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dtype: torch.dtype,
-               ksplit: int = 1, persistent: bool = False, ragged: bool = False) -> str:
-    """Fragment of the mangled name of pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT, PERSIST, RAGGED>."""
+               ksplit: int = 1, persistent: bool = False, ragged: bool = False, causal: bool = False) -> str:
+    """Fragment of the mangled name of
+    pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT, PERSIST, RAGGED, CAUSAL>."""
     return (f"fa_mfma_fwdI{MANGLED_T[dtype]}Li{d}ELi{br}ELi{bc}ELi{stages}E{MANGLED_T[out_dtype]}"
-            f"Li{ksplit}ELb{int(persistent)}ELb{int(ragged)}EE")
+            f"Li{ksplit}ELb{int(persistent)}ELb{int(ragged)}ELb{int(causal)}EE")
 
 
 def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal: bool, br: int) -> dict:
@@ -69,14 +70,14 @@ def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal:
     number of workgroups, read from the launcher's own description (pa_fused_tc_kernel), so the
     report names the kernel that actually runs."""
     if entry != "fused_tc":
-        return {"ksplit": 1, "persistent": False, "ragged": False, "workgroups": -(-n // br) * bh,
+        return {"ksplit": 1, "persistent": False, "ragged": False, "causal": False, "workgroups": -(-n // br) * bh,
                 "description": ""}
     code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
     desc = _native.fused_tc_kernel(code, code, bh, n, d, causal)
     grid = re.search(r"grid (\d+) x", desc)
     return {"ksplit": 2 if "key split 2" in desc else 1, "persistent": ", persistent" in desc,
-            "ragged": ", ragged" in desc, "workgroups": int(grid.group(1)) if grid else -(-n // br) * bh,
-            "description": desc}
+            "ragged": ", ragged" in desc, "causal": ", persistent, causal" in desc,
+            "workgroups": int(grid.group(1)) if grid else -(-n // br) * bh, "description": desc}
 
 
 def load_resources(path: str = RESOURCES) -> dict:
@@ -167,7 +168,7 @@ def evaluate(args) -> list[dict]:
         row.update(status="ok", median_ms=med, p10_ms=p10, p90_ms=p90, tflops=flops / (med * 1e-3) / 1e12)
         form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br)
         res = find_resources(res_all, kernel_key(dt, args.dim, br, bc, st, dt, form["ksplit"], form["persistent"],
-                                                 form["ragged"]))
+                                                 form["ragged"], form["causal"]))
         row["launch"] = form["description"]
         threads = br // 32 * 64 * form["ksplit"]   # one wave per 32 query rows per key group
         if res:

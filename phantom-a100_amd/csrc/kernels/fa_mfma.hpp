@@ -71,8 +71,8 @@
 //    loads) is hidden behind the previous block. When every tile is full (N a multiple of
 //    2 * BN, RAGGED = false) the mask code is compiled out and all but a block's last iteration
 //    take the fast path without a runtime test. RAGGED: the same walk for an even tile count
-//    whose last tile is partial; both wrap iterations then take the generic path and mask that
-//    tile.
+//    whose last tile is partial, or an odd count of full tiles padded with one empty tile; both
+//    wrap iterations then take the generic path and mask the tiles past N.
 //  * CAUSAL (the persistent form for causal rows, N a multiple of BM, B*H a multiple of 8): a
 //    block of query rows [q0, q0 + BM) sees its c = q0 / BN first key tiles unmasked in every
 //    wave, and then BM / BN diagonal tiles, of which wave w needs the first w / 2 + 1 (the last
@@ -279,9 +279,15 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   const int kv_end = causal ? min(N, q0 + BM) : N;
   // (CAUSAL: the block's tile counts, set again for every block of the walk.)
   int ntiles = (kv_end + BN - 1) / BN;
-  const int nit = (ntiles + KSPLIT - 1) / KSPLIT;   // iterations of every key group
   const int wave_kv_end = causal ? min(kv_end, q0w + 32) : kv_end;  // keys this wave can see
   int wave_tiles = (wave_kv_end + BN - 1) / BN;
+  // RAGGED with an odd tile count (every tile full): one more tile, entirely past N (it loads as
+  // zeros and is masked to P = 0), makes the count even for the wrap copies.
+  if constexpr (RAGGED) {
+    ntiles += ntiles & 1;
+    wave_tiles = ntiles;
+  }
+  const int nit = (ntiles + KSPLIT - 1) / KSPLIT;   // iterations of every key group
   // Tiles [0, clean_tiles) need no mask for this wave: all keys < N and (causal) all keys at or
   // before the wave's first query.
   const int clean_tiles = causal ? min(N / BN, (q0w + 1) / BN) : N / BN;

@@ -94,10 +94,10 @@ int persistent_from_env() {
 std::atomic<int> g_persistent{persistent_from_env()};
 bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) != 0; }
 
-// fused_tc, non-causal, an even number of key tiles: the persistent form. As many workgroups as
-// fit on the device at once (d = 128: one 8-wave workgroup per CU; d = 64 fp16: three 4-wave
-// workgroups per CU) each walk the query blocks of their XCD, so the next block's first tiles
-// load during the current block's last two. Measured on MI355X, TFLOP/s with one workgroup per
+// fused_tc, non-causal, an even number of key tiles or an odd number of full ones: the persistent
+// form. As many workgroups as fit on the device at once (d = 128: one 8-wave workgroup per CU;
+// d = 64 fp16: three 4-wave workgroups per CU) each walk the query blocks of their XCD, so the
+// next block's first tiles load during the current block's last two. Measured on MI355X, TFLOP/s with one workgroup per
 // query block -> persistent: B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024 at
 // d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
 // 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
@@ -108,7 +108,9 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // blocks of unequal length and ends with the most loaded CU).
 bool persistent_launch(bool tc, int stages, int ks, int64_t n, int bm, int bn, int64_t bh, int causal) {
   if (!(tc && stages == 2 && ks == 1 && persistent_enabled())) return false;
-  return causal ? (n % bm == 0 && bh % pa::kNumXcd == 0) : (n + bn - 1) / bn % 2 == 0;
+  // (An odd count of full tiles is padded with an empty one; a single tile is not, since a bf16
+  // row of one tile takes its P as two terms, which only the per-block launch does.)
+  return causal ? (n % bm == 0 && bh % pa::kNumXcd == 0) : ((n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn));
 }
 // Workgroups of the persistent launch: wgs_per_cu per CU, at most as many per XCD as the XCD has
 // blocks.
@@ -119,19 +121,36 @@ int persistent_grid(long long total_blocks, int wgs_per_cu) {
 
 // Workgroups of the persistent kernel that fit on one CU of the current device (queried once per
 // device), 0 if unknown.
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool CAUSAL>
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool RAGGED, bool CAUSAL>
 int persistent_wgs_per_cu() {
   static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false, CAUSAL>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, RAGGED, CAUSAL>,
                                                      BM / 32 * pa::kWave * KS, 0) != hipSuccess || n <= 0)
       return 0;
     cache[dev].store(n, std::memory_order_relaxed);
   }
   return n;
+}
+
+// Grid of the persistent launch of this call, 0 for one workgroup per query block. A call that
+// needs the RAGGED form keeps the persistent launch only if that kernel fits as many workgroups
+// per CU as the clean one: at d = 64 fp16 it needs 217 VGPRs (two workgroups per CU instead of
+// three), and there the per-block launch measured faster (4x16x4032 895 vs 864, 8x16x960 724 vs
+// 672 TFLOP/s), while at d = 128 (one workgroup per CU either way) padding an odd tile count
+// gained (bf16 4x32x4032 1190 -> 1221, 16x16x960 930 -> 960).
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
+int persistent_grid_for(int64_t n, int64_t bh, int causal) {
+  if (!persistent_launch(true, ST, KS, n, BM, BN, bh, causal)) return 0;
+  const long long total = (n + BM - 1) / BM * bh;
+  if (causal) return persistent_grid(total, persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, true>());
+  const int clean = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false>();
+  if (n % (2 * BN) == 0) return persistent_grid(total, clean);
+  const int ragged = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false>();
+  return ragged >= clean ? persistent_grid(total, ragged) : 0;
 }
 
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
@@ -141,15 +160,15 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
   if constexpr (TC && ST == 2 && KS == 1) {
-    if (persistent_launch(TC, ST, KS, n, BM, BN, bh, causal)) {
-      const int grid = persistent_grid(total, causal ? persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true>()
-                                                     : persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false>());
+    {
+      const int grid = persistent_grid_for<T, D, BM, BN, ST, OutT, KS>(n, bh, causal);
       if (grid > 0) {
-        // Non-causal with N a multiple of 2 * BN: every tile full. Otherwise (an even tile count
-        // whose last tile is partial) the RAGGED form, whose wrap copies mask that tile.
+        // Non-causal with N a multiple of 2 * BN: an even number of full tiles. Otherwise (an
+        // even tile count whose last tile is partial, or an odd count of full tiles, padded with
+        // an empty one) the RAGGED form, whose wrap copies mask the keys past N.
         auto kernel = causal ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false, true>
-                      : n % BN == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>
-                                    : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
+                      : n % (2 * BN) == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>
+                                          : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
         hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                            static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);
@@ -170,8 +189,7 @@ struct MfmaEntry {
   mfma_fn fn;
   int64_t lds;
   bool tc;                 // fused_tc entry: may take the persistent launch
-  int (*wgs_per_cu)();     // workgroups of its persistent kernel per CU (tc entries)
-  int (*wgs_per_cu_causal)();   // the same for its CAUSAL form
+  int (*persistent_grid)(int64_t n, int64_t bh, int causal);   // its persistent grid (tc entries)
 };
 
 template <typename T> constexpr int dt_code();
@@ -179,17 +197,16 @@ template <> constexpr int dt_code<pa::f16>() { return PA_DTYPE_F16; }
 template <> constexpr int dt_code<pa::bf16>() { return PA_DTYPE_BF16; }
 template <> constexpr int dt_code<float>() { return PA_DTYPE_F32; }
 
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool TC, bool CAUSAL>
-constexpr int (*wgs_per_cu_fn())() {
-  if constexpr (TC && ST == 2 && KS == 1) return &persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, CAUSAL>;
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool TC>
+constexpr int (*persistent_grid_fn())(int64_t, int64_t, int) {
+  if constexpr (TC && ST == 2 && KS == 1) return &persistent_grid_for<T, D, BM, BN, ST, OutT, KS>;
   else return nullptr;
 }
 
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
 constexpr MfmaEntry mfma_entry() {
   return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, KS, &launch_mfma<T, D, BM, BN, ST, OutT, KS, TC>,
-                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS, TC, wgs_per_cu_fn<T, D, BM, BN, ST, OutT, KS, TC, false>(),
-                   wgs_per_cu_fn<T, D, BM, BN, ST, OutT, KS, TC, true>()};
+                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS, TC, persistent_grid_fn<T, D, BM, BN, ST, OutT, KS, TC>()};
 }
 
 #define PA_TC_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T, 1, true>(), mfma_entry<T, D, BM, BN, ST, float, 1, true>()
@@ -420,14 +437,12 @@ const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, 
   if (!e) return "";
   static const char* dt_name[] = {"f32", "f16", "bf16"};
   const long long total = (n + e->br - 1) / e->br * bh;
-  int (*wgs)() = causal ? e->wgs_per_cu_causal : e->wgs_per_cu;
-  const int pgrid = persistent_launch(e->tc, e->db ? 2 : 1, e->ks, n, e->br, e->bc, bh, causal) && wgs
-                        ? persistent_grid(total, wgs()) : 0;
+  const int pgrid = e->persistent_grid ? e->persistent_grid(n, bh, causal) : 0;
   const bool pers = pgrid > 0;   // as in launch_mfma: no device (grid 0) means one workgroup per block
   snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s> grid %d x %d threads",
            dt_name[e->dtype], e->d, e->br, e->bc, e->db ? 2 : 1, dt_name[e->out_dtype],
            e->ks == 2 ? ", key split 2" : "", pers ? ", persistent" : "",
-           !pers ? "" : causal ? ", causal" : n % e->bc ? ", ragged" : "",
+           !pers ? "" : causal ? ", causal" : n % (2 * e->bc) ? ", ragged" : "",
            pers ? pgrid : (int)total, e->br / 32 * pa::kWave * e->ks);
   return desc;
 }

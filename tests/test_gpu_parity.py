@@ -370,7 +370,8 @@ def test_pipelined_kernels_repeat_bitwise(name, shape, dtype, causal, kw):
 # CUs, two key tiles per row (no regular iteration between the wrap copies), N = 8192, peaked rows
 # that rescale inside the wrap iterations, and ragged N (the RAGGED form: partial last tile), also
 # with more query blocks than workgroups (2048 and 1024 blocks, and 600 two-tile blocks), so that
-# a workgroup loads its next block's K(0), K(1), V(0) and Q after masking its partial last tile.
+# a workgroup loads its next block's K(0), K(1), V(0) and Q after masking its partial last tile;
+# and odd counts of full tiles, which the RAGGED form pads with one empty tile.
 PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype; d = 128
     ((4, 32, 4096), torch.bfloat16, 1.0, None),
     ((1, 64, 2048), torch.bfloat16, 1.0, torch.float32),
@@ -386,6 +387,9 @@ PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype; d = 128
     ((2, 40, 1024), torch.float16, 10.0, torch.float32),
     ((2, 16, 1000), torch.bfloat16, 1.0, None),          # ragged: last tile 40 keys
     ((1, 40, 100), torch.bfloat16, 3.0, torch.float32),  # ragged, two tiles
+    ((4, 32, 4032), torch.bfloat16, 1.0, None),          # 63 full tiles, padded to 64
+    ((2, 16, 960), torch.float16, 3.0, torch.float32),   # 15 full tiles
+    ((1, 40, 192), torch.bfloat16, 10.0, torch.float32), # 3 tiles, rescaling rows
     ((2, 16, 1000), torch.float16, 1.0, torch.float32),
     ((1, 40, 100), torch.float16, 3.0, None),
     ((4, 32, 4050), torch.bfloat16, 1.0, None),          # ragged, 2048 blocks: 8 per workgroup
@@ -411,13 +415,29 @@ def per_block_launch():
 PERSISTENT_SHAPES_D64 = [  # (B, H, N), dtype, qk_scale, out dtype; d = 64
     ((8, 16, 1024), torch.float16, 1.0, None),
     ((1, 16, 8192), torch.float16, 3.0, torch.float32),
-    ((2, 16, 1000), torch.float16, 1.0, torch.float32),
     ((1, 300, 128), torch.float16, 1.0, None),
     ((8, 16, 1024), torch.bfloat16, 1.0, None),
     ((1, 200, 100), torch.bfloat16, 3.0, torch.float32),   # (fewer heads take the key split)
     ((4, 16, 4050), torch.bfloat16, 1.0, None),
+    ((2, 16, 1000), torch.bfloat16, 1.0, torch.float32),
+    ((4, 16, 4032), torch.bfloat16, 1.0, None),           # 63 full tiles, padded to 64
+    ((1, 300, 192), torch.bfloat16, 3.0, torch.float32),  # three tiles, padded to four
 ]
 ALL_PERSISTENT = [(*c, 128) for c in PERSISTENT_SHAPES] + [(*c, 64) for c in PERSISTENT_SHAPES_D64]
+
+
+@pytest.mark.parametrize("n", [1000, 4032, 64])
+def test_fp16_d64_ragged_rows_take_the_per_block_launch(n):
+    """fp16 d = 64 rows that need the RAGGED form (a partial last tile, or an odd count of full
+    tiles) stay on the per-block launch: that kernel fits two workgroups per CU against the clean
+    persistent kernel's three, so the launcher keeps the per-block form, which is still correct."""
+    b, h = 2, 16
+    assert "persistent" in _native.fused_tc_kernel(_native.DTYPE_F16, _native.DTYPE_F16, b * h, 1024, 64)
+    desc = _native.fused_tc_kernel(_native.DTYPE_F16, _native.DTYPE_F16, b * h, n, 64)
+    assert "persistent" not in desc, desc
+    q, k, v = make_qkv(b, h, n, 64, torch.float16, seed=7, device="cuda")
+    out = cuda_attn.fused_tc(q, k, v, out_dtype=torch.float32)
+    assert max_err(out, f64_reference_gpu(q, k, v)) <= 2e-3
 
 
 @pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype, d", ALL_PERSISTENT)
