@@ -5,13 +5,16 @@
 //
 //   naive (/root/reference/csrc/kernels/naive.cuh:10-64): one thread per score, one thread per
 //         softmax row (three passes: max, sum, normalise), one thread per output element.
-//   tiled (/root/reference/csrc/kernels/tiled.cuh:16-117): 64x64 output tiles with 4x4 register
-//         blocking per thread and LDS-staged operands for both products; softmax with one wave
-//         per row (online max/sum per lane, then a 6-step butterfly merge across the 64 lanes);
-//         causal P.V skips key tiles right of the diagonal.
+//   tiled (/root/reference/csrc/kernels/tiled.cuh:16-117): the scores of fp16 inputs with d a
+//         multiple of 16 on the matrix core (128x128 tiles, tiled_scores_mfma), otherwise 64x64
+//         output tiles with 4x4 register blocking per thread and LDS-staged operands; softmax with
+//         one wave per row, the row held in registers up to 8192 keys (one read of S), else an
+//         online max/sum per lane and a 6-step butterfly merge across the 64 lanes; P.V with 4x4
+//         register blocking; causal P.V skips key tiles right of the diagonal.
 #pragma once
 
 #include "common.hpp"
+#include "fa_mfma.hpp"   // v_swz: the V tile layout of the fused kernel, reused by tiled_pv_mfma
 
 namespace pa {
 
@@ -122,7 +125,101 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float m2, float 
   m = mn;
 }
 
-// One wave per row, 4 rows per 256-thread workgroup.
+// S = scale * Q K^T on the matrix core, for fp16 storage and d = 16 * KSTEPS (the tiled_scores
+// result up to the order of the fp32 sums: products of fp16 values are exact in fp32). A 128 x 128
+// tile per workgroup, a 64 x 64 quarter per wave as 2 x 2 v_mfma_f32_32x32x16_f16 blocks, whose
+// operands are read straight from memory in the MFMA layout: lane l takes dims
+// 16 kk + 8 (l / 32) .. + 7 of row l % 32 of its 32-row block (16 bytes, rows 16-byte aligned);
+// rows past N read as zero through the buffer's range. Register r of a block holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4 and column l % 32, so each store instruction writes 128
+// contiguous bytes of two rows. With causal, a quarter entirely right of the diagonal skips its
+// products and stores -inf.
+template <int KSTEPS>
+__global__ void __launch_bounds__(256)
+tiled_scores_mfma(const f16* __restrict__ Q, const f16* __restrict__ K, float* __restrict__ S, int N,
+                  float scale, int causal) {
+  constexpr int D = 16 * KSTEPS;
+  const int bh = blockIdx.z;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int r0 = blockIdx.y * 128 + (wave / 2) * 64;
+  const int c0 = blockIdx.x * 128 + (wave % 2) * 64;
+  const int lr = lane % 32, hk = lane / 32;
+  const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(f16));
+  const rsrc_t q_rs = make_rsrc(Q + (size_t)bh * N * D, head_bytes);
+  const rsrc_t k_rs = make_rsrc(K + (size_t)bh * N * D, head_bytes);
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = f32x16{};
+  if (!(causal && c0 > r0 + 63)) {
+    f16x8 a[KSTEPS][2], b[KSTEPS][2];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        a[kk][x] = __builtin_bit_cast(f16x8, load16(q_rs, (uint32_t)(((r0 + 32 * x + lr) * D + 16 * kk + 8 * hk) * 2)));
+        b[kk][x] = __builtin_bit_cast(f16x8, load16(k_rs, (uint32_t)(((c0 + 32 * x + lr) * D + 16 * kk + 8 * hk) * 2)));
+      }
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32x32x16(a[kk][rb], b[kk][cb], acc[rb][cb]);
+  }
+  float* Sb = S + (size_t)bh * N * N;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = r0 + 32 * rb + 8 * (r / 4) + 4 * hk + r % 4;
+        const int j = c0 + 32 * cb + lr;
+        if (i < N && j < N) Sb[(size_t)i * N + j] = (causal && j > i) ? -INFINITY : acc[rb][cb][r] * scale;
+      }
+}
+
+// One wave per row, the whole row held in registers (rows of at most 64 * VPL keys): S is read
+// once and P written once, 8 bytes per score (the two-pass kernel below reads S twice). The max
+// first, then the sum of exp(x - max) kept in place, then P = e / sum; element j of the row sits in
+// lane j % 64, slot j / 64, so every load and store of a wave covers 256 contiguous bytes.
+template <int VPL>
+__global__ void __launch_bounds__(256)
+tiled_softmax_rows(float* __restrict__ S, int N) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int bh = blockIdx.y;
+  const int i = blockIdx.x * 4 + wave;
+  if (i >= N) return;  // whole wave leaves together
+  float* row = S + ((size_t)bh * N + i) * N;
+  float x[VPL];
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int j = lane + k * kWave;
+    x[k] = j < N ? row[j] : -INFINITY;
+    m = fmaxf(m, x[k]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  float l = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    x[k] = expf(x[k] - m);   // -inf (masked or past N) -> 0; every row has a finite score
+    l += x[k];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+  const float inv = 1.f / l;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int j = lane + k * kWave;
+    if (j < N) row[j] = x[k] * inv;
+  }
+}
+
+// One wave per row, 4 rows per 256-thread workgroup (rows longer than the register-held ones).
 __global__ void __launch_bounds__(256)
 tiled_softmax(float* __restrict__ S, int N) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -148,6 +245,121 @@ tiled_softmax(float* __restrict__ S, int N) {
   }
   const float inv = 1.f / l;
   for (int j = lane; j < N; j += kWave) row[j] = expf(row[j] - m) * inv;
+}
+
+// O = P V on the matrix core for fp16 V with D in {64, 128} (the fused kernel's V operand path),
+// computed transposed as O^T += V^T P^T per 16-key step with v_mfma_f32_32x32x16_f16: A = V^T,
+// read from a swizzled LDS tile of 64 keys with ds_read_b64_tr_b16; B = P^T, lane l taking the 8
+// probabilities of its query row l % 32 at the keys the V reads pair with them (two runs of 4
+// consecutive keys) straight from the fp32 workspace. P is fed as two fp16 terms of 1024 P (hi = round(1024 P), lo = round(1024 P - hi),
+// ~22 significant bits, the lo term clear of fp16's subnormals for P >= 2^-24), both products exact
+// in fp32 and summed in fp32; O is scaled back by 2^-10. 128 queries per workgroup (32 per wave),
+// two V stages; the next tile's V (to LDS) and P (to registers) load during the current one.
+// Reads past the head (query or key rows past N) return zero through the buffers' ranges, and
+// keys past N meet zero V rows. With causal, keys after the block's last query are skipped (their
+// P is zero).
+template <int D>
+__global__ void __launch_bounds__(256)
+tiled_pv_mfma(const float* __restrict__ P, const f16* __restrict__ V, f16* __restrict__ O, int N, int causal) {
+  constexpr int BN = 64, THREADS = 256, NDB = D / 32, CR = D / 8, RB = D * 2;
+  constexpr int TILE_BYTES = BN * RB;
+  constexpr int CPT = BN * CR / THREADS;   // 16-byte V chunks per thread per tile
+  static_assert(D == 64 || D == 128, "V layout of the fused kernel");
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds[2 * TILE_BYTES];
+  const int bh = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lq = lane % 32, hi = lane / 32;
+  const int q0 = blockIdx.x * 128;
+  const int qrow = q0 + wave * 32 + lq;
+  const rsrc_t v_rs = make_rsrc(V + (size_t)bh * N * D, (uint32_t)((size_t)N * D * sizeof(f16)));
+  const rsrc_t p_rs = make_rsrc(P + (size_t)bh * N * N, (uint32_t)((size_t)N * N * sizeof(float)));
+  uint32_t v_src[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int slot = i * THREADS + tid;
+    const int row = slot / CR, pc = slot % CR;
+    v_src[i] = (uint32_t)(row * RB + ((pc ^ v_swz<CR>(row)) * 16));
+  }
+  auto load_v = [&](int stage, int k0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      load16_to_lds(v_rs, v_lds + stage * TILE_BYTES + (i * THREADS + wave * kWave) * 16, v_src[i], (uint32_t)(k0 * RB));
+  };
+  const int g16 = lane / 16, i16 = lane % 16;
+  const int v_row = hi * 4 + i16 / 4;
+  const int v_cl = 2 * (g16 % 2) + (i16 % 4) / 2;
+  int v_addr[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    v_addr[db] = v_row * RB + (((4 * db + v_cl) ^ v_swz<CR>(v_row)) * 16) + 8 * (i16 % 2);
+  // P^T operands of one 64-key tile: for 16-key step ks, k-slot j of this lane holds key
+  // 16 ks + 8 (j / 4) + 4 hi + j % 4 of its query row, the key order in which the transposed
+  // V reads hand out the A operand (rows 4 hi .. 4 hi + 3, then 8 + 4 hi .. 8 + 4 hi + 3).
+  auto load_p = [&](u32x4 (&pr)[8], int k0) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        pr[2 * ks + h] = load16(p_rs, (uint32_t)(((size_t)qrow * N + k0 + 16 * ks + 8 * h + 4 * hi) * sizeof(float)));
+  };
+  f32x16 acc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
+  const int k_end = causal ? min(N, q0 + 128) : N;
+  const int ntiles = (k_end + BN - 1) / BN;
+  u32x4 pc[8], pn[8];
+  load_v(0, 0);
+  load_p(pc, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) {
+      load_v((t + 1) & 1, (t + 1) * BN);
+      load_p(pn, (t + 1) * BN);
+    }
+    const unsigned char* vs = v_lds + (t & 1) * TILE_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      f16x8 ph, pl;
+      // (the whole u32x4 is bit-cast to f32x4: casting one element of a loaded u32x4 to float
+      // miscompiles with this hipcc, every element then reading element 0)
+      const f32x4 p4[2] = {__builtin_bit_cast(f32x4, pc[2 * ks]), __builtin_bit_cast(f32x4, pc[2 * ks + 1])};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = 1024.f * p4[j / 4][j % 4];
+        const f16 h = (f16)x;
+        ph[j] = h;
+        pl[j] = (f16)(x - (float)h);
+      }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const unsigned char* p0 = vs + ks * 16 * RB + v_addr[db];
+        const i16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)(p0));
+        const i16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)(p0 + 8 * RB));
+        const f16x8 a = __builtin_bit_cast(f16x8, i16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]});
+        acc[db] = mfma32x32x16(a, ph, acc[db]);
+        acc[db] = mfma32x32x16(a, pl, acc[db]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pc[i] = pn[i];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  // Register r of block db holds dim 32 db + 8 (r / 4) + 4 hi + r % 4 of query qrow.
+  if (qrow < N) {
+    f16* orow = O + ((size_t)bh * N + qrow) * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        typedef f16 F16x4 __attribute__((ext_vector_type(4)));
+        F16x4 w;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) w[rr] = (f16)(acc[db][g4 * 4 + rr] * (1.f / 1024.f));
+        *reinterpret_cast<F16x4*>(orow + db * 32 + g4 * 8 + hi * 4) = w;
+      }
+  }
 }
 
 // O[i0:i0+64, c0:c0+64] = P_rows . V_cols; with causal, P is zero right of the diagonal so

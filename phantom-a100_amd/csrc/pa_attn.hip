@@ -290,11 +290,54 @@ hipError_t launch_tiled(const void* q, const void* k, const void* v, void* o, fl
                         int causal, hipStream_t stream) {
   const float scale = 1.f / sqrtf((float)d);
   const int nt = (n + pa::kTile - 1) / pa::kTile;
-  hipLaunchKernelGGL(pa::tiled_scores<T>, dim3(nt, nt, bh), dim3(256), 0, stream, static_cast<const T*>(q),
-                     static_cast<const T*>(k), s, n, d, scale, causal);
-  hipLaunchKernelGGL(pa::tiled_softmax, dim3((n + 3) / 4, bh), dim3(256), 0, stream, s, n);
-  hipLaunchKernelGGL(pa::tiled_pv<T>, dim3((d + pa::kTile - 1) / pa::kTile, nt, bh), dim3(256), 0, stream, s,
-                     static_cast<const T*>(v), static_cast<T*>(o), n, d, causal);
+  bool mfma_scores = false;
+  if constexpr (std::is_same<T, pa::f16>::value) {
+    // fp16 rows of 16 * {2, 4, 5, 6, 8} dims, 16-byte aligned, one head below 2 GiB.
+    const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0;
+    const int nt128 = (n + 127) / 128;
+    auto launch = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(nt128, nt128, bh), dim3(256), 0, stream, static_cast<const pa::f16*>(q),
+                         static_cast<const pa::f16*>(k), s, n, scale, causal);
+      mfma_scores = true;
+    };
+    if (aligned && (int64_t)n * d * 2 < (1ll << 31)) {
+      switch (d) {
+        case 32: launch(pa::tiled_scores_mfma<2>); break;
+        case 64: launch(pa::tiled_scores_mfma<4>); break;
+        case 80: launch(pa::tiled_scores_mfma<5>); break;
+        case 96: launch(pa::tiled_scores_mfma<6>); break;
+        case 128: launch(pa::tiled_scores_mfma<8>); break;
+        default: break;
+      }
+    }
+  }
+  if (!mfma_scores)
+    hipLaunchKernelGGL(pa::tiled_scores<T>, dim3(nt, nt, bh), dim3(256), 0, stream, static_cast<const T*>(q),
+                       static_cast<const T*>(k), s, n, d, scale, causal);
+  const dim3 sm_grid((n + 3) / 4, bh);
+  if (n <= 256) hipLaunchKernelGGL(pa::tiled_softmax_rows<4>, sm_grid, dim3(256), 0, stream, s, n);
+  else if (n <= 1024) hipLaunchKernelGGL(pa::tiled_softmax_rows<16>, sm_grid, dim3(256), 0, stream, s, n);
+  else if (n <= 2048) hipLaunchKernelGGL(pa::tiled_softmax_rows<32>, sm_grid, dim3(256), 0, stream, s, n);
+  else if (n <= 4096) hipLaunchKernelGGL(pa::tiled_softmax_rows<64>, sm_grid, dim3(256), 0, stream, s, n);
+  else if (n <= 8192) hipLaunchKernelGGL(pa::tiled_softmax_rows<128>, sm_grid, dim3(256), 0, stream, s, n);
+  else hipLaunchKernelGGL(pa::tiled_softmax, sm_grid, dim3(256), 0, stream, s, n);
+  bool mfma_pv = false;
+  if constexpr (std::is_same<T, pa::f16>::value) {
+    // fp16 V with d in {64, 128}, 16-byte aligned rows of P (N a multiple of 4) and V, one head's
+    // P and V each below 2 GiB.
+    const bool ok = (d == 64 || d == 128) && n % 4 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(s) % 16 == 0 && (int64_t)n * n * 4 < (1ll << 31) &&
+                    (int64_t)n * d * 2 < (1ll << 31);
+    if (ok) {
+      auto kernel = d == 64 ? pa::tiled_pv_mfma<64> : pa::tiled_pv_mfma<128>;
+      hipLaunchKernelGGL(kernel, dim3((n + 127) / 128, bh), dim3(256), 0, stream, s, static_cast<const pa::f16*>(v),
+                         static_cast<pa::f16*>(o), n, causal);
+      mfma_pv = true;
+    }
+  }
+  if (!mfma_pv)
+    hipLaunchKernelGGL(pa::tiled_pv<T>, dim3((d + pa::kTile - 1) / pa::kTile, nt, bh), dim3(256), 0, stream, s,
+                       static_cast<const T*>(v), static_cast<T*>(o), n, d, causal);
   return hipGetLastError();
 }
 
