@@ -97,8 +97,9 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // fused_tc, non-causal, an even number of key tiles or an odd number of full ones: the persistent
 // form. As many workgroups as fit on the device at once (d = 128: one 8-wave workgroup per CU;
 // d = 64 fp16: three 4-wave workgroups per CU) each walk the query blocks of their XCD, so the
-// next block's first tiles load during the current block's last two. Measured on MI355X, TFLOP/s with one workgroup per
-// query block -> persistent: B x H x N = 4x32x4096 / 2x16x8192 / 1x64x2048 / 16x16x1024 at
+// next block's first tiles load during the current block's last two. Measured on MI355X,
+// TFLOP/s with one workgroup per query block -> persistent: B x H x N = 4x32x4096 / 2x16x8192 /
+// 1x64x2048 / 16x16x1024 at
 // d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
 // 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
 // C5 845 -> 890 (back to back), 605 -> 627 and 821 -> 859 under the flushing protocol.
@@ -106,8 +107,10 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // XCD can own whole heads (B*H a multiple of 8): its workgroups walk their XCD's heads round by
 // round, so each gets the same number of key tiles (the per-block launch leaves CUs idle between
 // blocks of unequal length and ends with the most loaded CU).
-bool persistent_launch(bool tc, int stages, int ks, int64_t n, int bm, int bn, int64_t bh, int causal) {
-  if (!(tc && stages == 2 && ks == 1 && persistent_enabled())) return false;
+// (Only the two-stage fused_tc kernels without a key split have persistent forms; the caller,
+// persistent_grid_for, is instantiated for those alone.)
+bool persistent_launch(int64_t n, int bm, int bn, int64_t bh, int causal) {
+  if (!persistent_enabled()) return false;
   // (An odd count of full tiles is padded with an empty one; a single tile is not, since a bf16
   // row of one tile takes its P as two terms, which only the per-block launch does.)
   return causal ? (n % bm == 0 && bh % pa::kNumXcd == 0) : ((n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn));
@@ -144,7 +147,8 @@ int persistent_wgs_per_cu() {
 // gained (bf16 4x32x4032 1190 -> 1221, 16x16x960 930 -> 960).
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
 int persistent_grid_for(int64_t n, int64_t bh, int causal) {
-  if (!persistent_launch(true, ST, KS, n, BM, BN, bh, causal)) return 0;
+  static_assert(ST == 2 && KS == 1, "persistent forms: two stages, no key split");
+  if (!persistent_launch(n, BM, BN, bh, causal)) return 0;
   const long long total = (n + BM - 1) / BM * bh;
   if (causal) return persistent_grid(total, persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, true>());
   const int clean = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false>();

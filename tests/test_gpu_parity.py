@@ -123,6 +123,18 @@ def test_other_head_dims_for_unfused(name, d):
     assert max_err(cuda_attn.KERNELS[name](q, k, v), cuda_attn.reference(q, k, v)) <= 1e-4
 
 
+@pytest.mark.parametrize("d", [32, 64, 80, 96, 128])
+@pytest.mark.parametrize("n", [200, 333, 1024])
+@pytest.mark.parametrize("causal", [False, True])
+def test_tiled_fp16_head_dims(d, n, causal):
+    """tiled with fp16 inputs at every head dim the matrix-core scores kernel is compiled for
+    (16 x {2, 4, 5, 6, 8}; P.V on the matrix core at d in {64, 128} with N a multiple of 4, so
+    N = 333 keeps the VALU P.V), against float64."""
+    q, k, v = gpu_qkv(1, 3, n, d, torch.float16, seed=5)
+    out = cuda_attn.tiled(q, k, v, causal)
+    assert max_err(out, f64_reference_gpu(q, k, v, causal)) <= 2e-3
+
+
 @pytest.mark.parametrize("name", ["fused", "fused_vec"])
 def test_fused_rejects_unsupported_head_dim(name):
     q, k, v = gpu_qkv(1, 1, 64, 128, torch.float16)
