@@ -5,12 +5,13 @@
 //
 //   naive (/root/reference/csrc/kernels/naive.cuh:10-64): one thread per score, one thread per
 //         softmax row (three passes: max, sum, normalise), one thread per output element.
-//   tiled (/root/reference/csrc/kernels/tiled.cuh:16-117): the scores of fp16 inputs with d a
-//         multiple of 16 on the matrix core (128x128 tiles, tiled_scores_mfma), otherwise 64x64
-//         output tiles with 4x4 register blocking per thread and LDS-staged operands; softmax with
-//         one wave per row, the row held in registers up to 8192 keys (one read of S), else an
-//         online max/sum per lane and a 6-step butterfly merge across the 64 lanes; P.V with 4x4
-//         register blocking; causal P.V skips key tiles right of the diagonal.
+//   tiled (/root/reference/csrc/kernels/tiled.cuh:16-117): both products on the matrix core
+//         for fp16 inputs (scores at d a multiple of 16, P.V at d = 64 / 128) and for fp32 inputs
+//         at d = 64 / 128 (tiled_*_mfma, tiled_*_mfma_f32); otherwise 64x64 output tiles with 4x4
+//         register blocking per thread and LDS-staged operands. Softmax with one wave per row,
+//         the row held in registers up to 8192 keys (one read of S), else an online max/sum per
+//         lane and a 6-step butterfly merge across the 64 lanes. Causal P.V skips key tiles right
+//         of the diagonal.
 #pragma once
 
 #include "common.hpp"
@@ -167,6 +168,64 @@ tiled_scores_mfma(const f16* __restrict__ Q, const f16* __restrict__ K, float* _
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32x32x16(a[kk][rb], b[kk][cb], acc[rb][cb]);
+  }
+  float* Sb = S + (size_t)bh * N * N;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = r0 + 32 * rb + 8 * (r / 4) + 4 * hk + r % 4;
+        const int j = c0 + 32 * cb + lr;
+        if (i < N && j < N) Sb[(size_t)i * N + j] = (causal && j > i) ? -INFINITY : acc[rb][cb][r] * scale;
+      }
+}
+
+// S = scale * Q K^T on the fp32 matrix core (v_mfma_f32_32x32x2_f32) for fp32 storage and
+// D in {64, 128}; the tiled_scores result up to the order of its fp32 sums. 128 x 128 tile per
+// workgroup, 64 x 64 per wave as 2 x 2 blocks. The dot product's dims are walked in an order that
+// keeps every lane's reads contiguous: within each 64-dim chunk, k-step kk of lane l takes dim
+// 32 (l / 32) + kk of its row (l % 32 of the block), in Q and K alike, so a lane reads 32
+// consecutive floats (8 x 16 bytes) per row and chunk. Rows past N read as zero.
+template <int D>
+__global__ void __launch_bounds__(256)
+tiled_scores_mfma_f32(const float* __restrict__ Q, const float* __restrict__ K, float* __restrict__ S, int N,
+                      float scale, int causal) {
+  static_assert(D % 64 == 0, "64-dim chunks");
+  const int bh = blockIdx.z;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int r0 = blockIdx.y * 128 + (wave / 2) * 64;
+  const int c0 = blockIdx.x * 128 + (wave % 2) * 64;
+  const int lr = lane % 32, hk = lane / 32;
+  const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(float));
+  const rsrc_t q_rs = make_rsrc(Q + (size_t)bh * N * D, head_bytes);
+  const rsrc_t k_rs = make_rsrc(K + (size_t)bh * N * D, head_bytes);
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = f32x16{};
+  if (!(causal && c0 > r0 + 63)) {
+#pragma unroll 1
+    for (int ch = 0; ch < D / 64; ++ch) {
+      f32x4 a[2][8], b[2][8];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const uint32_t col = (uint32_t)(64 * ch + 32 * hk + 4 * v);
+          a[x][v] = __builtin_bit_cast(f32x4, load16(q_rs, (uint32_t)((r0 + 32 * x + lr) * D + col) * 4));
+          b[x][v] = __builtin_bit_cast(f32x4, load16(k_rs, (uint32_t)((c0 + 32 * x + lr) * D + col) * 4));
+        }
+#pragma unroll
+      for (int kk = 0; kk < 32; ++kk)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            acc[rb][cb] = mfma32x32x2(a[rb][kk / 4][kk % 4], b[cb][kk / 4][kk % 4], acc[rb][cb]);
+    }
   }
   float* Sb = S + (size_t)bh * N * N;
 #pragma unroll
@@ -360,6 +419,86 @@ tiled_pv_mfma(const float* __restrict__ P, const f16* __restrict__ V, f16* __res
         *reinterpret_cast<F16x4*>(orow + db * 32 + g4 * 8 + hi * 4) = w;
       }
   }
+}
+
+// O = P V on the fp32 matrix core for fp32 V and D in {64, 128}: A = P (lane l: 32 consecutive
+// probabilities of its query row l % 32 per 64-key tile, the keys of k-step kk being
+// 32 (l / 32) + kk, read straight from the workspace), B = V from a 64-key LDS tile (lane l reads
+// key 32 (l / 32) + kk, dim l % 32 of its 32-dim block). 128 queries per workgroup, 32 per wave;
+// the next tile's V (to LDS) and P (to registers) load during the current one. Reads past the
+// head return zero; keys past N meet zero V rows. With causal, keys after the block's last query
+// are skipped.
+template <int D>
+__global__ void __launch_bounds__(256)
+tiled_pv_mfma_f32(const float* __restrict__ P, const float* __restrict__ V, float* __restrict__ O, int N, int causal) {
+  constexpr int BN = 64, THREADS = 256, NDB = D / 32;
+  constexpr int ROW = D + 4;                       // LDS row pitch in floats (padding spreads banks)
+  static_assert(D == 64 || D == 128, "head dim");
+  __shared__ __attribute__((aligned(16))) float v_lds[2][BN * ROW];
+  const int bh = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lq = lane % 32, hi = lane / 32;
+  const int q0 = blockIdx.x * 128;
+  const int qrow = q0 + wave * 32 + lq;
+  const rsrc_t v_rs = make_rsrc(V + (size_t)bh * N * D, (uint32_t)((size_t)N * D * sizeof(float)));
+  const rsrc_t p_rs = make_rsrc(P + (size_t)bh * N * N, (uint32_t)((size_t)N * N * sizeof(float)));
+  // V tile: 64 keys x D floats, 16 bytes per thread per load, rows of D / 4 chunks.
+  constexpr int CH = BN * D / 4 / THREADS;
+  auto load_v = [&](u32x4 (&vr)[CH], int k0) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int slot = i * THREADS + tid, row = slot / (D / 4), c4 = slot % (D / 4);
+      vr[i] = load16(v_rs, (uint32_t)(((k0 + row) * D + 4 * c4) * 4));
+    }
+  };
+  auto store_v = [&](const u32x4 (&vr)[CH], int stage) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int slot = i * THREADS + tid, row = slot / (D / 4), c4 = slot % (D / 4);
+      *reinterpret_cast<f32x4*>(&v_lds[stage][row * ROW + 4 * c4]) = __builtin_bit_cast(f32x4, vr[i]);
+    }
+  };
+  auto load_p = [&](u32x4 (&pr)[8], int k0) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      pr[v] = load16(p_rs, (uint32_t)(((size_t)qrow * N + k0 + 32 * hi + 4 * v) * sizeof(float)));
+  };
+  f32x16 acc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
+  const int k_end = causal ? min(N, q0 + 128) : N;
+  const int ntiles = (k_end + BN - 1) / BN;
+  u32x4 vr[CH], pc[8], pn[8];
+  load_v(vr, 0);
+  load_p(pc, 0);
+  store_v(vr, 0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const bool more = t + 1 < ntiles;
+    if (more) {
+      load_v(vr, (t + 1) * BN);
+      load_p(pn, (t + 1) * BN);
+    }
+    const float* vs = v_lds[t & 1];
+#pragma unroll
+    for (int kk = 0; kk < 32; ++kk) {
+      const float a = __builtin_bit_cast(f32x4, pc[kk / 4])[kk % 4];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] = mfma32x32x2(a, vs[(32 * hi + kk) * ROW + 32 * db + lq], acc[db]);
+    }
+    if (more) store_v(vr, (t + 1) & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pc[i] = pn[i];
+    __syncthreads();
+  }
+  // Register r of block db holds query 8 (r / 4) + 4 hi + r % 4 of the wave and dim 32 db + l % 32.
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int q = q0 + wave * 32 + 8 * (r / 4) + 4 * hi + r % 4;
+      if (q < N) O[((size_t)bh * N + q) * D + 32 * db + lq] = acc[db][r];
+    }
 }
 
 // O[i0:i0+64, c0:c0+64] = P_rows . V_cols; with causal, P is zero right of the diagonal so

@@ -315,6 +315,17 @@ hipError_t launch_tiled(const void* q, const void* k, const void* v, void* o, fl
       }
     }
   }
+  if constexpr (std::is_same<T, float>::value) {
+    // fp32 rows of 64 or 128 dims, 16-byte aligned, one head below 2 GiB.
+    const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0;
+    if (aligned && (d == 64 || d == 128) && (int64_t)n * d * 4 < (1ll << 31)) {
+      const int nt128 = (n + 127) / 128;
+      hipLaunchKernelGGL(d == 64 ? pa::tiled_scores_mfma_f32<64> : pa::tiled_scores_mfma_f32<128>,
+                         dim3(nt128, nt128, bh), dim3(256), 0, stream, static_cast<const float*>(q),
+                         static_cast<const float*>(k), s, n, scale, causal);
+      mfma_scores = true;
+    }
+  }
   if (!mfma_scores)
     hipLaunchKernelGGL(pa::tiled_scores<T>, dim3(nt, nt, bh), dim3(256), 0, stream, static_cast<const T*>(q),
                        static_cast<const T*>(k), s, n, d, scale, causal);
@@ -336,6 +347,16 @@ hipError_t launch_tiled(const void* q, const void* k, const void* v, void* o, fl
       auto kernel = d == 64 ? pa::tiled_pv_mfma<64> : pa::tiled_pv_mfma<128>;
       hipLaunchKernelGGL(kernel, dim3((n + 127) / 128, bh), dim3(256), 0, stream, s, static_cast<const pa::f16*>(v),
                          static_cast<pa::f16*>(o), n, causal);
+      mfma_pv = true;
+    }
+  }
+  if constexpr (std::is_same<T, float>::value) {
+    const bool ok = (d == 64 || d == 128) && n % 4 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(s) % 16 == 0 && (int64_t)n * n * 4 < (1ll << 31) &&
+                    (int64_t)n * d * 4 < (1ll << 31);
+    if (ok) {
+      hipLaunchKernelGGL(d == 64 ? pa::tiled_pv_mfma_f32<64> : pa::tiled_pv_mfma_f32<128>, dim3((n + 127) / 128, bh),
+                         dim3(256), 0, stream, s, static_cast<const float*>(v), static_cast<float*>(o), n, causal);
       mfma_pv = true;
     }
   }
