@@ -63,8 +63,9 @@
 //    merges them with the online-softmax rule and stores.
 //  * STAGES == 1: no prefetch (the reference's v3.1 structure): load tile, wait, compute.
 //  * Workgroup ids are remapped so that all query blocks of a head run on one XCD (shared L2).
-//  * PERSIST (two stages, no key split; launched for non-causal rows whose tile count is even):
-//    as many workgroups as fit at once walk the query blocks of their XCD's range. The last two
+//  * PERSIST (two stages, no key split; launched for non-causal rows with an even tile count or
+//    an odd count of full tiles): as many workgroups as fit at once walk the query blocks of
+//    their XCD's range. The last two
 //    iterations of a block are separate copies of the iteration (compile-time WRAP) whose loads
 //    past the block's last tile fetch the next block's K(0), K(1), V(0) and Q, so a block starts
 //    with its first tiles already in LDS and the per-block start-up (workgroup launch, first
@@ -77,12 +78,13 @@
 //    block of query rows [q0, q0 + BM) sees its c = q0 / BN first key tiles unmasked in every
 //    wave, and then BM / BN diagonal tiles, of which wave w needs the first w / 2 + 1 (the last
 //    one masked). The c clean tiles run the clean persistent iterations; the diagonal tiles (with
-//    the two before them) run copies whose fast/generic/idle choice is made per wave at run time
-//    and whose fast path masks S(t+1) when t+1 is the wave's diagonal tile. Blocks are dealt to
-//    the workgroups of an XCD in rounds of whole heads (longest block first within a head), in a
-//    serpentine order: the workgroup that gets a round's c-th longest block gets the next
-//    round's c-th shortest, so every workgroup gets the same number of tiles, while the blocks
-//    running at once on an XCD share the K/V of few heads in its L2.
+//    the two before them) run copies (DIAG) in which each wave takes the fast path up to its last
+//    tile and idles after it, the fast path masking S(t+1) when t+1 is the wave's diagonal tile;
+//    only the block's very last tile (the last wrap copy) takes the generic path. Blocks are
+//    dealt to the workgroups of an XCD in rounds of whole heads (longest block first within a
+//    head), in a serpentine order: the workgroup that gets a round's c-th longest block gets the
+//    next round's c-th shortest, so every workgroup gets the same number of tiles, while the
+//    blocks running at once on an XCD share the K/V of few heads in its L2.
 #pragma once
 
 #include <type_traits>
