@@ -18,21 +18,32 @@ from cuda_attn.workloads import make_qkv
 
 pytestmark = pytest.mark.gpu
 
+# (entry, shape, dtype, causal, kwargs); the first GRAPH_CASES also run under graph capture (the
+# unfused entries allocate their score workspace per call). The causal fused_tc cases take the
+# causal persistent launch (B*H a multiple of 8, N a multiple of the query block).
 CASES = [
-    ("fused_tc", (2, 8, 512, 128), torch.bfloat16, {}),
-    ("fused_tc", (2, 8, 1000, 64), torch.float16, {}),
-    ("fused_tuned", (1, 8, 512, 64), torch.float16, {"br": 128, "bc": 64, "double_buffer": True}),
-    ("fused", (1, 8, 256, 64), torch.float32, {}),
-    ("tiled", (1, 4, 256, 64), torch.float32, {}),
+    ("fused_tc", (2, 8, 512, 128), torch.bfloat16, False, {}),
+    ("fused_tc", (2, 8, 1000, 64), torch.float16, False, {}),
+    ("fused_tc", (2, 8, 1024, 128), torch.bfloat16, True, {}),
+    ("fused_tc", (2, 8, 512, 64), torch.float16, True, {}),
+    ("fused_tuned", (1, 8, 512, 64), torch.float16, False, {"br": 128, "bc": 64, "double_buffer": True}),
+    ("fused", (1, 8, 256, 64), torch.float32, False, {}),
+    ("tiled", (1, 4, 256, 64), torch.float32, False, {}),
+    ("tiled", (1, 4, 512, 64), torch.float16, True, {}),
 ]
+GRAPH_CASES = 6
 
 
-@pytest.mark.parametrize("name, shape, dtype, kw", CASES, ids=[c[0] + "-" + str(c[2])[6:] for c in CASES])
-def test_side_streams_match_default_stream(name, shape, dtype, kw):
-    print(f"[streams] {name} {shape} {dtype}", flush=True)
+def case_id(c):
+    return f"{c[0]}-{str(c[2])[6:]}" + ("-causal" if c[3] else "")
+
+
+@pytest.mark.parametrize("name, shape, dtype, causal, kw", CASES, ids=[case_id(c) for c in CASES])
+def test_side_streams_match_default_stream(name, shape, dtype, causal, kw):
+    print(f"[streams] {name} {shape} {dtype} causal={causal}", flush=True)
     fn = getattr(cuda_attn, name)
     inputs = [make_qkv(*shape, dtype, seed=60 + i, device="cuda") for i in range(3)]
-    want = [fn(q, k, v, False, **kw) for q, k, v in inputs]
+    want = [fn(q, k, v, causal, **kw) for q, k, v in inputs]
     torch.cuda.synchronize()
     streams = [torch.cuda.Stream() for _ in inputs]
     got = [None] * len(inputs)
@@ -40,7 +51,7 @@ def test_side_streams_match_default_stream(name, shape, dtype, kw):
         for i, ((q, k, v), s) in enumerate(zip(inputs, streams)):
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):
-                got[i] = fn(q, k, v, False, **kw)
+                got[i] = fn(q, k, v, causal, **kw)
         for s in streams:
             torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
@@ -65,19 +76,19 @@ def test_launch_uses_the_current_stream():
         assert torch.equal(out, want), f"trial {trial}"
 
 
-@pytest.mark.parametrize("name, shape, dtype, kw", CASES[:4], ids=[c[0] + "-" + str(c[2])[6:] for c in CASES[:4]])
-def test_graph_capture_replays_match_eager(name, shape, dtype, kw):
-    print(f"[graph] {name} {shape} {dtype}", flush=True)
+@pytest.mark.parametrize("name, shape, dtype, causal, kw", CASES[:GRAPH_CASES], ids=[case_id(c) for c in CASES[:GRAPH_CASES]])
+def test_graph_capture_replays_match_eager(name, shape, dtype, causal, kw):
+    print(f"[graph] {name} {shape} {dtype} causal={causal}", flush=True)
     fn = getattr(cuda_attn, name)
     q, k, v = (t.clone() for t in make_qkv(*shape, dtype, seed=80, device="cuda"))
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):                    # warm-up outside the graph, as torch requires
-        fn(q, k, v, False, **kw)
+        fn(q, k, v, causal, **kw)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = fn(q, k, v, False, **kw)
+        out = fn(q, k, v, causal, **kw)
     for replay in range(4):
         nq, nk, nv = make_qkv(*shape, dtype, seed=90 + replay, device="cuda")
         q.copy_(nq)
@@ -86,6 +97,6 @@ def test_graph_capture_replays_match_eager(name, shape, dtype, kw):
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
-        want = fn(nq, nk, nv, False, **kw)        # eager, between replays
+        want = fn(nq, nk, nv, causal, **kw)       # eager, between replays
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {replay}"
