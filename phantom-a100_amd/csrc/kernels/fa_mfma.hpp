@@ -85,6 +85,8 @@
 //    head), in a serpentine order: the workgroup that gets a round's c-th longest block gets the
 //    next round's c-th shortest, so every workgroup gets the same number of tiles, while the
 //    blocks running at once on an XCD share the K/V of few heads in its L2.
+//  * The persistent forms stage each wave's block of O in LDS and store it as whole rows with
+//    non-temporal stores (store_block), so few dirty O lines are left for the end of the launch.
 #pragma once
 
 #include <type_traits>
@@ -106,19 +108,22 @@ struct MfmaLds {
 template <int CR> __device__ __forceinline__ int k_swz(int row) { return CR == 16 ? (row & 15) : ((row >> 1) & 7); }
 template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 16 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); }
 
-// Minimum waves per SIMD the register allocator must allow (0: compiler default).
+// Minimum waves per SIMD the register allocator must allow (1: no constraint; PA_MFMA_MIN_WAVES
+// overrides it for every instantiation). The fp16 d = 64 causal persistent form keeps three
+// 4-wave workgroups per CU only within 168 VGPRs (unconstrained it takes 169).
 #ifndef PA_MFMA_MIN_WAVES
 #define PA_MFMA_MIN_WAVES 0
 #endif
-#if PA_MFMA_MIN_WAVES > 0
-#define PA_MFMA_OCCUPANCY __attribute__((amdgpu_waves_per_eu(PA_MFMA_MIN_WAVES)))
-#else
-#define PA_MFMA_OCCUPANCY
-#endif
+template <typename T, int D, bool PERSIST, bool CAUSAL>
+constexpr int mfma_min_waves() {
+  return PA_MFMA_MIN_WAVES > 0 ? PA_MFMA_MIN_WAVES
+                               : (PERSIST && CAUSAL && D == 64 && !std::is_same<T, bf16>::value) ? 3 : 1;
+}
 
 template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false,
           bool RAGGED = false, bool CAUSAL = false>
-__global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT) PA_MFMA_OCCUPANCY
+__global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT)
+__attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, CAUSAL>())))
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
   typedef typename vec8<T>::type V8;
@@ -155,6 +160,17 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[L::TILE_BYTES * KSPLIT];
   __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[STAGES == 2 ? L::TILE_BYTES * KSPLIT : 16];
   __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[STAGES == 2 ? L::TILE_BYTES * KSPLIT : 16];
+  // Persistent forms: each wave's block of O goes through its own LDS rows and leaves as whole
+  // rows, 16 bytes per lane, in ORW-row passes that fit kOStage bytes per workgroup (three
+  // d = 64 workgroups per CU: 3 x (32 + 16) KB; one d = 128 workgroup: 64 + 64 KB). The smaller
+  // alignment places o_lds after the K/V stages, which keep their ds_read immediate offsets.
+  constexpr int OROW = D * (int)sizeof(OutT);          // bytes of one O row
+  constexpr int OCR = OROW / 16;                       // its 16-byte chunks
+  constexpr int kOStage = D == 64 ? 16384 : 65536;
+  constexpr int OPASS = PERSIST ? (NW * 32 * OROW + kOStage - 1) / kOStage : 1;
+  constexpr int ORW = 32 / OPASS;                      // rows of a wave per pass
+  static_assert(32 % OPASS == 0 && (ORW * OCR) % kWave == 0, "O passes: whole rows, whole wave reads");
+  __shared__ __attribute__((aligned(16))) unsigned char o_lds[PERSIST ? NW * ORW * OROW : 16];
   const std::integral_constant<int, 0> even{};
   const std::integral_constant<int, 1> odd{};
 
@@ -394,16 +410,55 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   };
 
   // O = O^T / l for the current block. Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
+  // Persistent forms: through the wave's LDS rows (16-byte chunks XOR-swizzled by row), then
+  // non-temporal 16-byte buffer stores that each cover whole rows. O is written once and not
+  // read again, and whole-row stores let the lines leave L2 during the kernel instead of with the
+  // cache writeback at its end (C3 +4 %; stores of the lane's 8-byte pieces, non-temporal or
+  // write-through, were 13-15 % slower). Rows past N fall outside the buffer and are dropped.
   auto store_block = [&]() {
     const float l_tot = lacc[0];
     const float inv = 1.f / l_tot;
-    if (g == 0 && qrow < N) {
+    typedef OutT OutV4 __attribute__((ext_vector_type(4)));
+    if constexpr (PERSIST) {
+      constexpr int kNonTemporal = 2;   // buffer store cache policy: nt
+      unsigned char* ws = o_lds + wave * ORW * OROW;
+      const rsrc_t o_rs = make_rsrc(O + base, (uint32_t)((size_t)N * OROW));
+      // Lane-derived offsets behind an empty asm: hoisted out of the block loop they cost ~14 VGPRs.
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int lq_ = ln % 32, hi_ = ln / 32;
+#pragma unroll
+      for (int p = 0; p < OPASS; ++p) {
+        if (lq_ / ORW == p) {
+          const int row = lq_ % ORW;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              OutV4 w;
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);
+              const int byte = (32 * db + 8 * g4 + 4 * hi_) * (int)sizeof(OutT);
+              *reinterpret_cast<OutV4*>(ws + row * OROW + (((byte / 16) ^ (row % OCR)) * 16) + byte % 16) = w;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's rows are in LDS
+#pragma unroll
+        for (int i = 0; i < ORW * OCR / kWave; ++i) {
+          const int c16 = i * kWave + ln, row = c16 / OCR, c = c16 % OCR;
+          const u32x4 d = *reinterpret_cast<const u32x4*>(ws + row * OROW + ((c ^ (row % OCR)) * 16));
+          // (fp32 O: a head can span up to 4 GiB, so the offset is unsigned.)
+          __builtin_amdgcn_raw_buffer_store_b128(d, o_rs, (uint32_t)(q0w + p * ORW + row) * (uint32_t)OROW + c * 16, 0,
+                                                 kNonTemporal);
+        }
+        if (p + 1 < OPASS) __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next pass
+      }
+    } else if (g == 0 && qrow < N) {
       OutT* orow = O + base + (size_t)qrow * D;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-          typedef OutT OutV4 __attribute__((ext_vector_type(4)));
           OutV4 w;
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);

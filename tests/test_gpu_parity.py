@@ -428,6 +428,8 @@ PERSISTENT_SHAPES_D64 = [  # (B, H, N), dtype, qk_scale, out dtype; d = 64
     ((8, 16, 1024), torch.float16, 1.0, None),
     ((1, 16, 8192), torch.float16, 3.0, torch.float32),
     ((1, 300, 128), torch.float16, 1.0, None),
+    ((8, 64, 256), torch.float16, 3.0, None),             # 1024 blocks of four tiles
+    ((8, 300, 128), torch.float16, 10.0, torch.float32),  # 2400 two-tile blocks, ~3 per workgroup
     ((8, 16, 1024), torch.bfloat16, 1.0, None),
     ((1, 200, 100), torch.bfloat16, 3.0, torch.float32),   # (fewer heads take the key split)
     ((4, 16, 4050), torch.bfloat16, 1.0, None),
