@@ -8,7 +8,7 @@ Same harness behaviour and CSV schema as the reference's bench/benchmark.py:106-
     result outside the gate is written as ``wrong_result`` and never timed;
   * timing: warm-up calls, then per timed call a zeroing of a flush buffer followed by one call
     between two HIP events; median and 10th / 90th percentiles;
-  * peak device memory of one call (torch caching-allocator statistics);
+  * peak device memory of one call above what was live before it (caching-allocator statistics);
   * configurations that cannot run are status rows, not crashes: ``unavailable`` (flash-attn is
     not installed on ROCm here), ``fp16_only``, ``unsupported_d``, ``skipped_oom`` (the N x N
     score workspace of naive / tiled / sdpa_math would not fit), ``oom``, ``error``.
@@ -21,10 +21,10 @@ from __future__ import annotations
 import argparse
 import csv
 import os
-import statistics
 import sys
 from datetime import datetime, timezone
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
@@ -117,39 +117,43 @@ def status_before_run(name: str, dtype: torch.dtype, d: int) -> str | None:
 
 
 def time_calls(fn, warmup: int, iters: int, flush_buf: torch.Tensor):
-    """Median, p10, p90 in ms of `iters` calls, each after a cache flush, HIP-event timed on the
-    current stream."""
+    """(median, p10, p90) in ms of `iters` calls under the reference's timing protocol
+    (/root/reference/bench/benchmark.py:78-93, whose steps are kept so the numbers compare):
+    untimed warm-up calls, then for every timed call a rewrite of `flush_buf` (so every cache level
+    starts cold), the call between two HIP events on the current stream, and a host wait for it."""
+    stream = torch.cuda.current_stream()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    times = []
-    for _ in range(iters):
+    samples = []
+    while len(samples) < iters:
         flush_buf.zero_()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
+        begin.record(stream)
         fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1))
-    return summarize(times)
+        end.record(stream)
+        end.synchronize()
+        samples.append(begin.elapsed_time(end))
+    return summarize(samples)
 
 
-def summarize(times: list[float]):
-    times = sorted(times)
-    if len(times) == 1:
-        return times[0], times[0], times[0]
-    q = statistics.quantiles(times, n=10)
-    return statistics.median(times), q[0], q[-1]
+def summarize(times) -> tuple[float, float, float]:
+    """Median, 10th and 90th percentile (linear interpolation between order statistics)."""
+    med, p10, p90 = np.percentile(np.asarray(times, dtype=np.float64), [50, 10, 90])
+    return float(med), float(p10), float(p90)
 
 
-def peak_memory_mb(fn) -> float:
+def allocated_peak_mb(fn) -> float:
+    """MiB the caching allocator held at its peak during one call above what was live before it
+    (outputs and workspaces; the reference's peak_mem_mb column)."""
     torch.cuda.synchronize()
+    live = torch.cuda.memory_stats().get("allocated_bytes.all.current", 0)
     torch.cuda.reset_peak_memory_stats()
-    base = torch.cuda.memory_allocated()
-    fn()
+    result = fn()
     torch.cuda.synchronize()
-    return (torch.cuda.max_memory_allocated() - base) / 2**20
+    peak = torch.cuda.memory_stats().get("allocated_bytes.all.peak", live)
+    del result
+    return (peak - live) / 2**20
 
 
 def device_meta() -> dict:
@@ -159,33 +163,87 @@ def device_meta() -> dict:
                 timestamp=datetime.now(timezone.utc).isoformat(timespec="seconds"))
 
 
-def run_point(name, q, k, v, causal, ref, args, flush_buf, row) -> dict:
-    """One (impl, shape) measurement -> completed CSV row."""
-    b, h, n, d = q.shape
-    st = status_before_run(name, q.dtype, d)
-    if st:
-        return dict(row, status=st)
-    free, _ = torch.cuda.mem_get_info()
-    if not fits_in_memory(name, b, h, n, d, q.element_size(), free):
-        return dict(row, status="skipped_oom")
-    fn_raw = IMPLS[name]
-    fn = lambda: fn_raw(q, k, v, causal)  # noqa: E731
-    try:
-        err = gate_error(fn(), ref) if ref is not None else float("nan")
-        if err > gate_tolerance(q.dtype, causal, v.abs().max().item()):
-            return dict(row, max_abs_err=f"{err:.2e}", status="wrong_result")
-        iters = args.iters if name != "naive" or n <= 2048 else max(10, args.iters // 10)
-        med, p10, p90 = time_calls(fn, args.warmup, iters, flush_buf)
-        mem = peak_memory_mb(fn)
-    except torch.cuda.OutOfMemoryError:
-        torch.cuda.empty_cache()
-        return dict(row, status="oom")
-    except RuntimeError as e:
-        print(f"{name} N={n}: {e}", file=sys.stderr)
-        return dict(row, status="error")
-    tflops = attention_flops(b, h, n, d, causal) / (med * 1e-3) / 1e12
-    return dict(row, median_ms=f"{med:.4f}", p10_ms=f"{p10:.4f}", p90_ms=f"{p90:.4f}", tflops=f"{tflops:.3f}",
-                peak_mem_mb=f"{mem:.1f}", max_abs_err=f"{err:.2e}", status="ok")
+class Sweep:
+    """One benchmark run: the (causal, N) grid of input shapes, every implementation at each, one
+    CSV row per (shape, implementation) written as soon as it is measured."""
+
+    def __init__(self, args):
+        self.args = args
+        self.dtype = DTYPES[args.dtype]
+        self.meta = device_meta()
+        l2 = torch.cuda.get_device_properties(0).L2_cache_size
+        self.flush = torch.empty(max(2 * l2, FLUSH_BYTES_MIN), dtype=torch.uint8, device="cuda")
+        self.gen = torch.Generator().manual_seed(0)
+
+    def shapes(self):
+        modes = {"off": (False,), "on": (True,), "both": (False, True)}[self.args.causal]
+        return [(causal, n) for causal in modes for n in self.args.ns]
+
+    def inputs(self, n: int):
+        a = self.args
+        return [torch.randn(a.batch, a.heads, n, a.dim, generator=self.gen).to(self.dtype).cuda() for _ in range(3)]
+
+    def measure(self, name: str, q, k, v, causal: bool, ref) -> dict:
+        """The CSV row of one implementation at one shape: a status row if it cannot run here, else
+        gated against the fp32 reference, then timed and its allocation peak taken."""
+        b, h, n, d = q.shape
+        row = dict(self.meta, impl=name, dtype=self.args.dtype, causal=causal, B=b, H=h, N=n, d=d)
+        status = status_before_run(name, q.dtype, d)
+        if status is None and not fits_in_memory(name, b, h, n, d, q.element_size(), torch.cuda.mem_get_info()[0]):
+            status = "skipped_oom"
+        if status is not None:
+            row["status"] = status
+            return row
+        impl = IMPLS[name]
+
+        def call():
+            return impl(q, k, v, causal)
+
+        try:
+            err = gate_error(call(), ref) if ref is not None else float("nan")
+            if err > gate_tolerance(q.dtype, causal, v.abs().max().item()):
+                row.update(max_abs_err=f"{err:.2e}", status="wrong_result")
+                return row
+            # naive re-reads S from HBM three times per call: fewer timed calls past N = 2048
+            iters = self.args.iters if name != "naive" or n <= 2048 else max(10, self.args.iters // 10)
+            med, p10, p90 = time_calls(call, self.args.warmup, iters, self.flush)
+            mem = allocated_peak_mb(call)
+        except torch.cuda.OutOfMemoryError:
+            torch.cuda.empty_cache()
+            row["status"] = "oom"
+            return row
+        except RuntimeError as e:
+            print(f"{name} N={n}: {e}", file=sys.stderr)
+            row["status"] = "error"
+            return row
+        tflops = attention_flops(b, h, n, d, causal) / (med * 1e-3) / 1e12
+        row.update(median_ms=f"{med:.4f}", p10_ms=f"{p10:.4f}", p90_ms=f"{p90:.4f}", tflops=f"{tflops:.3f}",
+                   peak_mem_mb=f"{mem:.1f}", max_abs_err=f"{err:.2e}", status="ok")
+        return row
+
+    def run(self, out: str) -> None:
+        print(f"# {self.meta}")
+        with open(out, "w", newline="") as fh:
+            writer = csv.DictWriter(fh, fieldnames=FIELDS)
+            writer.writeheader()
+            for causal, n in self.shapes():
+                q, k, v = self.inputs(n)
+                ref = cuda_attn.reference(q, k, v, causal) if n <= self.args.ref_max_n else None
+                for name in self.args.impls:
+                    row = self.measure(name, q, k, v, causal, ref)
+                    writer.writerow(row)
+                    fh.flush()
+                    print(report_line(row))
+                del q, k, v, ref
+                torch.cuda.empty_cache()
+
+
+def report_line(row: dict) -> str:
+    head = f"{row['impl']:12} N={row['N']:<5} causal={int(bool(row['causal']))}"
+    if row.get("status") != "ok":
+        return f"{head}  {row.get('status')}"
+    return (f"{head}  {float(row['median_ms']):9.3f} ms  {float(row['tflops']):8.2f} TFLOP/s  "
+            f"peak {float(row['peak_mem_mb']):8.1f} MiB  err {row['max_abs_err']}")
 
 
 def parse_args(argv=None):
@@ -208,36 +266,10 @@ def main(argv=None) -> str:
     args = parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("benchmark.py needs a GPU")
-    dtype = DTYPES[args.dtype]
-    meta = device_meta()
-    out = args.out or os.path.join("results", "measured", f"bench_{meta['gpu'].replace(' ', '_')}.csv")
+    sweep = Sweep(args)
+    out = args.out or os.path.join("results", "measured", f"bench_{sweep.meta['gpu'].replace(' ', '_')}.csv")
     os.makedirs(os.path.dirname(out) or ".", exist_ok=True)
-    causal_modes = {"off": [False], "on": [True], "both": [False, True]}[args.causal]
-    l2 = torch.cuda.get_device_properties(0).L2_cache_size
-    flush_buf = torch.empty(max(2 * l2, FLUSH_BYTES_MIN), dtype=torch.uint8, device="cuda")
-    print(f"# {meta}")
-    gen = torch.Generator().manual_seed(0)
-    with open(out, "w", newline="") as fh:
-        w = csv.DictWriter(fh, fieldnames=FIELDS)
-        w.writeheader()
-        for causal in causal_modes:
-            for n in args.ns:
-                b, h, d = args.batch, args.heads, args.dim
-                q, k, v = (torch.randn(b, h, n, d, generator=gen).to(dtype).cuda() for _ in range(3))
-                ref = cuda_attn.reference(q, k, v, causal) if n <= args.ref_max_n else None
-                for name in args.impls:
-                    row = dict(meta, impl=name, dtype=args.dtype, causal=causal, B=b, H=h, N=n, d=d)
-                    res = run_point(name, q, k, v, causal, ref, args, flush_buf, row)
-                    w.writerow(res)
-                    fh.flush()
-                    if res["status"] == "ok":
-                        print(f"causal={causal!s:5} N={n:5} {name:12} {float(res['median_ms']):9.3f} ms  "
-                              f"{float(res['tflops']):8.2f} TFLOP/s  {float(res['peak_mem_mb']):9.1f} MB  "
-                              f"err={res['max_abs_err']}")
-                    else:
-                        print(f"causal={causal!s:5} N={n:5} {name:12} {res['status']}")
-                del q, k, v, ref
-                torch.cuda.empty_cache()
+    sweep.run(out)
     print(f"wrote {out}")
     return out
 

@@ -3,8 +3,8 @@
 // They exist for API completeness and as an independent GPU cross-check of the fused kernels;
 // any head dim d >= 1 is accepted, fp32 or fp16 storage, fp32 arithmetic.
 //
-//   naive (/root/reference/csrc/kernels/naive.cuh:10-64): one thread per score, one thread per
-//         softmax row (three passes: max, sum, normalise), one thread per output element.
+//   naive (/root/reference/csrc/kernels/naive.cuh:10-64): the same three passes (scores, softmax
+//         by row max / sum / normalise, P.V) as plain loops, one wave per row of each product.
 //   tiled (/root/reference/csrc/kernels/tiled.cuh:16-117): both products on the matrix core
 //         for fp16 inputs (scores at d a multiple of 16, P.V at d = 64 / 128) and for fp32 inputs
 //         at d = 64 / 128 (tiled_*_mfma, tiled_*_mfma_f32); otherwise 64x64 output tiles with 4x4
@@ -20,47 +20,64 @@
 namespace pa {
 
 // ------------------------------------------------------------------------------------ naive
+// The reference's three unfused passes, each a plain loop per lane, laid out by waves: every
+// workgroup is 4 waves, and a wave owns one row of the product it writes (64 keys of a score row,
+// a whole softmax row, 64 head dims of an output row), so the operand that row shares (the query
+// row, the P row) is the same address in every lane, and the per-lane operand (a K row, a V
+// column) is a different one. Grids are flattened into x: N rows times column blocks.
+
+// S[h][i][j0 + lane] for the wave's query row i and 64 keys from j0; keys after i are -inf when
+// causal.
 template <typename T>
 __global__ void __launch_bounds__(256)
 naive_scores(const T* __restrict__ Q, const T* __restrict__ K, float* __restrict__ S, int N, int d,
-             float scale, int causal) {
-  const int bh = blockIdx.z;
-  const int i = blockIdx.y * 4 + threadIdx.y;
-  const int j = blockIdx.x * 64 + threadIdx.x;
+             float scale, int causal, int key_blocks) {
+  const int unit = (int)blockIdx.x * 4 + (int)threadIdx.x / kWave;   // (query row, 64-key block)
+  const int i = unit / key_blocks;
+  const int j = (unit % key_blocks) * kWave + (int)threadIdx.x % kWave;
   if (i >= N || j >= N) return;
-  const T* q = Q + ((size_t)bh * N + i) * d;
-  const T* k = K + ((size_t)bh * N + j) * d;
-  float acc = 0.f;
-  for (int c = 0; c < d; ++c) acc = fmaf(to_f32(q[c]), to_f32(k[c]), acc);
-  S[((size_t)bh * N + i) * N + j] = (causal && j > i) ? -INFINITY : acc * scale;
+  const size_t head = (size_t)blockIdx.y * N;
+  const T* qi = Q + (head + i) * d;
+  const T* kj = K + (head + j) * d;
+  float dot = 0.f;
+  for (int c = 0; c < d; ++c) dot = fmaf(to_f32(qi[c]), to_f32(kj[c]), dot);
+  float* srow = S + (head + i) * N;
+  srow[j] = (causal && j > i) ? -INFINITY : scale * dot;
 }
 
+// Row r of S in place: max, sum of exp(s - max), then exp(s - max) / sum, each a strided pass
+// of the wave's 64 lanes over the row followed by a butterfly reduction across the lanes.
 __global__ void __launch_bounds__(256)
-naive_softmax(float* __restrict__ S, int N) {
-  const int bh = blockIdx.y;
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= N) return;
-  float* row = S + ((size_t)bh * N + i) * N;
-  float m = -INFINITY;
-  for (int j = 0; j < N; ++j) m = fmaxf(m, row[j]);
-  float l = 0.f;
-  for (int j = 0; j < N; ++j) l += expf(row[j] - m);
-  const float inv = 1.f / l;
-  for (int j = 0; j < N; ++j) row[j] = expf(row[j] - m) * inv;
+naive_softmax(float* __restrict__ S, int N, long long rows) {
+  const long long r = (long long)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (r >= rows) return;
+  const int lane = (int)threadIdx.x % kWave;
+  float* srow = S + r * N;
+  float mx = -INFINITY;
+  for (int j = lane; j < N; j += kWave) mx = fmaxf(mx, srow[j]);
+  for (int w = kWave / 2; w >= 1; w /= 2) mx = fmaxf(mx, __shfl_xor(mx, w));
+  float sum = 0.f;
+  for (int j = lane; j < N; j += kWave) sum += expf(srow[j] - mx);
+  for (int w = kWave / 2; w >= 1; w /= 2) sum += __shfl_xor(sum, w);
+  const float rcp = 1.f / sum;
+  for (int j = lane; j < N; j += kWave) srow[j] = expf(srow[j] - mx) * rcp;
 }
 
+// O[h][i][c0 + lane] = sum over keys j of P[h][i][j] V[h][j][c0 + lane], for the wave's row i and
+// 64 head dims from c0.
 template <typename T>
 __global__ void __launch_bounds__(256)
-naive_pv(const float* __restrict__ P, const T* __restrict__ V, T* __restrict__ O, int N, int d) {
-  const int bh = blockIdx.z;
-  const int i = blockIdx.y * 4 + threadIdx.y;
-  const int c = blockIdx.x * 64 + threadIdx.x;
+naive_pv(const float* __restrict__ P, const T* __restrict__ V, T* __restrict__ O, int N, int d, int dim_blocks) {
+  const int unit = (int)blockIdx.x * 4 + (int)threadIdx.x / kWave;   // (query row, 64-dim block)
+  const int i = unit / dim_blocks;
+  const int c = (unit % dim_blocks) * kWave + (int)threadIdx.x % kWave;
   if (i >= N || c >= d) return;
-  const float* p = P + ((size_t)bh * N + i) * N;
-  const T* v = V + (size_t)bh * N * d;
+  const size_t head = (size_t)blockIdx.y * N;
+  const float* pi = P + (head + i) * N;
+  const T* vc = V + head * d + c;
   float acc = 0.f;
-  for (int j = 0; j < N; ++j) acc = fmaf(p[j], to_f32(v[(size_t)j * d + c]), acc);
-  O[((size_t)bh * N + i) * d + c] = from_f32<T>(acc);
+  for (int j = 0; j < N; ++j) acc = fmaf(pi[j], to_f32(vc[(size_t)j * d]), acc);
+  O[(head + i) * d + c] = from_f32<T>(acc);
 }
 
 // ------------------------------------------------------------------------------------ tiled

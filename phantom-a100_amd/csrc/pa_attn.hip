@@ -281,11 +281,17 @@ template <typename T>
 hipError_t launch_naive(const void* q, const void* k, const void* v, void* o, float* s, int bh, int n, int d,
                         int causal, hipStream_t stream) {
   const float scale = 1.f / sqrtf((float)d);
-  hipLaunchKernelGGL(pa::naive_scores<T>, dim3((n + 63) / 64, (n + 3) / 4, bh), dim3(64, 4), 0, stream,
-                     static_cast<const T*>(q), static_cast<const T*>(k), s, n, d, scale, causal);
-  hipLaunchKernelGGL(pa::naive_softmax, dim3((n + 255) / 256, bh), dim3(256), 0, stream, s, n);
-  hipLaunchKernelGGL(pa::naive_pv<T>, dim3((d + 63) / 64, (n + 3) / 4, bh), dim3(64, 4), 0, stream, s,
-                     static_cast<const T*>(v), static_cast<T*>(o), n, d);
+  // Four waves per workgroup, one wave per (row, 64 columns); the heads in y.
+  const long long key_blocks = (n + 63) / 64, dim_blocks = (d + 63) / 64;
+  const long long score_units = (long long)n * key_blocks, pv_units = (long long)n * dim_blocks;
+  const long long rows = (long long)n * bh;
+  if (score_units > INT_MAX - 4 || pv_units > INT_MAX - 4 || (rows + 3) / 4 > INT_MAX)   // 32-bit unit indices
+    return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(pa::naive_scores<T>, dim3((unsigned)((score_units + 3) / 4), bh), dim3(256), 0, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k), s, n, d, scale, causal, (int)key_blocks);
+  hipLaunchKernelGGL(pa::naive_softmax, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, s, n, rows);
+  hipLaunchKernelGGL(pa::naive_pv<T>, dim3((unsigned)((pv_units + 3) / 4), bh), dim3(256), 0, stream, s,
+                     static_cast<const T*>(v), static_cast<T*>(o), n, d, (int)dim_blocks);
   return hipGetLastError();
 }
 

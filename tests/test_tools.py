@@ -100,6 +100,16 @@ def test_bf16_causal_gate_allows_one_rounded_weight():
     assert benchmark.gate_tolerance(torch.float16, causal=True, vmax=4.0) == 2e-3
 
 
+def test_tile_sweep_points_and_rows():
+    """The tile sweep loads by path (as the GPU test does) and covers every compiled tile."""
+    sw = load("pa_sweep_tiles", os.path.join(PKG, "bench", "sweep_tiles.py"))
+    assert sorted(sw.tile_points()) == sorted((br, bc, db) for br, bc in ((64, 32), (64, 64), (128, 32), (128, 64))
+                                              for db in (False, True))
+    assert sw.TileRun(256, 64, 32, True).csv_row("gpu") == ["gpu", 256, 64, 32, True, "", "", "ok"]
+    assert sw.TileRun(256, 64, 32, False, "ok", 1.5, 2.25).csv_row("gpu")[5:] == ["1.5000", "2.250", "ok"]
+    assert sw.FIELDS == ["gpu", "N", "br", "bc", "double_buffer", "median_ms", "tflops", "status"]
+
+
 def test_flush_buffer_exceeds_infinity_cache():
     assert benchmark.FLUSH_BYTES_MIN > 256 * 2**20
 
@@ -275,9 +285,9 @@ def test_rules_fire_on_their_evidence():
     }
     assert set(cases) == set(dg.THRESHOLDS)
     for rule, counters in cases.items():
-        got = [b.name for b in dg.diagnose(counters, comp)]
+        got = [f.rule for f in dg.diagnose(counters, comp)]
         assert rule in got, (rule, got)
-        assert all(b.severity >= 1 for b in dg.diagnose(counters, comp))
+        assert all(f.score >= 1 for f in dg.diagnose(counters, comp))
 
 
 def test_clean_point_triggers_nothing():
