@@ -426,6 +426,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       // Lane-derived offsets behind an empty asm: hoisted out of the block loop they cost ~14 VGPRs.
       int ln = lane;
       asm volatile("" : "+v"(ln));
+      // Chunk swizzle of a staged row: 128-byte rows (8 chunks) pair up rows as the K tiles do, so
+      // the 32 rows written at one chunk spread over all 64 banks; longer rows XOR by row % chunks.
+      auto o_swz = [](int row) { return OCR == 8 ? (row >> 1) & 7 : row % OCR; };
       const int lq_ = ln % 32, hi_ = ln / 32;
 #pragma unroll
       for (int p = 0; p < OPASS; ++p) {
@@ -439,14 +442,14 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 #pragma unroll
               for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);
               const int byte = (32 * db + 8 * g4 + 4 * hi_) * (int)sizeof(OutT);
-              *reinterpret_cast<OutV4*>(ws + row * OROW + (((byte / 16) ^ (row % OCR)) * 16) + byte % 16) = w;
+              *reinterpret_cast<OutV4*>(ws + row * OROW + (((byte / 16) ^ o_swz(row)) * 16) + byte % 16) = w;
             }
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's rows are in LDS
 #pragma unroll
         for (int i = 0; i < ORW * OCR / kWave; ++i) {
           const int c16 = i * kWave + ln, row = c16 / OCR, c = c16 % OCR;
-          const u32x4 d = *reinterpret_cast<const u32x4*>(ws + row * OROW + ((c ^ (row % OCR)) * 16));
+          const u32x4 d = *reinterpret_cast<const u32x4*>(ws + row * OROW + ((c ^ o_swz(row)) * 16));
           // (fp32 O: a head can span up to 4 GiB, so the offset is unsigned.)
           __builtin_amdgcn_raw_buffer_store_b128(d, o_rs, (uint32_t)(q0w + p * ORW + row) * (uint32_t)OROW + c * 16, 0,
                                                  kNonTemporal);
