@@ -102,6 +102,19 @@ struct MfmaLds {
   static constexpr int BYTES = STAGES * 2 * TILE_BYTES;   // K stages then V stages
 };
 
+// The persistent forms' O staging rows: each wave stages its 32 rows of O in ROWS-row passes that
+// fit LIMIT bytes per workgroup (three d = 64 workgroups per CU: 3 x (32 + 16) KB; one d = 128
+// workgroup: 64 + 64 KB), so BYTES of LDS per workgroup beside the K/V stages.
+template <int D, int BM, typename OutT>
+struct MfmaOStage {
+  static constexpr int ROW = D * (int)sizeof(OutT);       // bytes of one O row
+  static constexpr int CHUNKS = ROW / 16;                  // its 16-byte chunks
+  static constexpr int LIMIT = D == 64 ? 16384 : 65536;
+  static constexpr int PASSES = (BM * ROW + LIMIT - 1) / LIMIT;
+  static constexpr int ROWS = 32 / PASSES;                 // rows of a wave per pass
+  static constexpr int BYTES = BM / 32 * ROWS * ROW;
+};
+
 // XOR swizzle of the 16-byte chunk index within a row (CR chunks per row).
 // K: consecutive rows r..r+15 read at one logical chunk land in 16 distinct bank groups.
 // V: rows r..r+3 (r % 4 == 0) x chunks 4q..4q+3 land in 16 distinct bank groups.
@@ -109,15 +122,17 @@ template <int CR> __device__ __forceinline__ int k_swz(int row) { return CR == 1
 template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 16 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); }
 
 // Minimum waves per SIMD the register allocator must allow (1: no constraint; PA_MFMA_MIN_WAVES
-// overrides it for every instantiation). The fp16 d = 64 causal persistent form keeps three
-// 4-wave workgroups per CU only within 168 VGPRs (unconstrained it takes 169).
+// overrides it for every instantiation). Three 4-wave d = 64 workgroups per CU need at most 168
+// VGPRs: the fp16 causal persistent form takes 169 unconstrained, the bf16 non-causal persistent
+// forms 169-171 (held to 168 they spill 1-2 VGPRs and still run 3.5-6 % faster; the bf16 causal
+// form, at 193-195, stays at two).
 #ifndef PA_MFMA_MIN_WAVES
 #define PA_MFMA_MIN_WAVES 0
 #endif
 template <typename T, int D, bool PERSIST, bool CAUSAL>
 constexpr int mfma_min_waves() {
   return PA_MFMA_MIN_WAVES > 0 ? PA_MFMA_MIN_WAVES
-                               : (PERSIST && CAUSAL && D == 64 && !std::is_same<T, bf16>::value) ? 3 : 1;
+                               : (PERSIST && D == 64 && (std::is_same<T, bf16>::value ? !CAUSAL : CAUSAL)) ? 3 : 1;
 }
 
 template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false,
@@ -160,17 +175,16 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[L::TILE_BYTES * KSPLIT];
   __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[STAGES == 2 ? L::TILE_BYTES * KSPLIT : 16];
   __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[STAGES == 2 ? L::TILE_BYTES * KSPLIT : 16];
-  // Persistent forms: each wave's block of O goes through its own LDS rows and leaves as whole
-  // rows, 16 bytes per lane, in ORW-row passes that fit kOStage bytes per workgroup (three
-  // d = 64 workgroups per CU: 3 x (32 + 16) KB; one d = 128 workgroup: 64 + 64 KB). The smaller
-  // alignment places o_lds after the K/V stages, which keep their ds_read immediate offsets.
-  constexpr int OROW = D * (int)sizeof(OutT);          // bytes of one O row
-  constexpr int OCR = OROW / 16;                       // its 16-byte chunks
-  constexpr int kOStage = D == 64 ? 16384 : 65536;
-  constexpr int OPASS = PERSIST ? (NW * 32 * OROW + kOStage - 1) / kOStage : 1;
-  constexpr int ORW = 32 / OPASS;                      // rows of a wave per pass
-  static_assert(32 % OPASS == 0 && (ORW * OCR) % kWave == 0, "O passes: whole rows, whole wave reads");
-  __shared__ __attribute__((aligned(16))) unsigned char o_lds[PERSIST ? NW * ORW * OROW : 16];
+  // Persistent forms: each wave's block of O goes through its own LDS rows (MfmaOStage) and leaves
+  // as whole rows, 16 bytes per lane. The smaller alignment places o_lds after the K/V stages,
+  // which keep their ds_read immediate offsets.
+  typedef MfmaOStage<D, BM, OutT> OS;
+  constexpr int OROW = OS::ROW;
+  constexpr int OCR = OS::CHUNKS;
+  constexpr int OPASS = PERSIST ? OS::PASSES : 1;
+  constexpr int ORW = OS::ROWS;
+  static_assert(32 % OS::PASSES == 0 && (ORW * OCR) % kWave == 0, "O passes: whole rows, whole wave reads");
+  __shared__ __attribute__((aligned(16))) unsigned char o_lds[PERSIST ? OS::BYTES : 16];
   const std::integral_constant<int, 0> even{};
   const std::integral_constant<int, 1> odd{};
 

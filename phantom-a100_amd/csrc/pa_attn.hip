@@ -96,7 +96,7 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 
 // fused_tc, non-causal, an even number of key tiles or an odd number of full ones: the persistent
 // form. As many workgroups as fit on the device at once (d = 128: one 8-wave workgroup per CU;
-// d = 64 fp16: three 4-wave workgroups per CU) each walk the query blocks of their XCD, so the
+// d = 64: three 4-wave workgroups per CU) each walk the query blocks of their XCD, so the
 // next block's first tiles load during the current block's last two. Measured on MI355X,
 // TFLOP/s with one workgroup per query block -> persistent: B x H x N = 4x32x4096 / 2x16x8192 /
 // 1x64x2048 / 16x16x1024 at
@@ -209,8 +209,11 @@ constexpr int (*persistent_grid_fn())(int64_t, int64_t, int) {
 
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
 constexpr MfmaEntry mfma_entry() {
+  // LDS: the K/V stages, plus the O staging rows where the entry can take a persistent form.
+  constexpr int64_t lds = (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS +
+                          (persistent_grid_fn<T, D, BM, BN, ST, OutT, KS, TC>() ? pa::MfmaOStage<D, BM, OutT>::BYTES : 0);
   return MfmaEntry{dt_code<T>(), dt_code<OutT>(), D, BM, BN, ST == 2 ? 1 : 0, KS, &launch_mfma<T, D, BM, BN, ST, OutT, KS, TC>,
-                   (int64_t)pa::MfmaLds<D, BN, ST>::BYTES * KS, TC, persistent_grid_fn<T, D, BM, BN, ST, OutT, KS, TC>()};
+                   lds, TC, persistent_grid_fn<T, D, BM, BN, ST, OutT, KS, TC>()};
 }
 
 #define PA_TC_BOTH_OUT(T, D, BM, BN, ST) mfma_entry<T, D, BM, BN, ST, T, 1, true>(), mfma_entry<T, D, BM, BN, ST, float, 1, true>()

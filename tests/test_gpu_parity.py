@@ -421,9 +421,9 @@ def per_block_launch():
     _native.set_persistent(prev)
 
 
-# The same check for the d = 64 persistent launch (fp16: three 4-wave workgroups per CU, bf16:
-# two): the C3 and C5 shapes (1024 blocks on 768 / 512 workgroups, so some workgroups walk two
-# blocks and some one), ragged N, and two-tile rows on many blocks.
+# The same check for the d = 64 persistent launch (three 4-wave workgroups per CU): the C3 and C5
+# shapes (1024 blocks on 768 workgroups, so some workgroups walk two blocks and some one), ragged N,
+# and two-tile rows on many blocks.
 PERSISTENT_SHAPES_D64 = [  # (B, H, N), dtype, qk_scale, out dtype; d = 64
     ((8, 16, 1024), torch.float16, 1.0, None),
     ((1, 16, 8192), torch.float16, 3.0, torch.float32),
