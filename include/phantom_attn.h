@@ -114,7 +114,8 @@ int pa_set_persistent(int enable);
  * Replaces fused_tuned_smem_bytes (csrc/kernels/fused_tuned.cuh:188-190). No GPU needed. */
 int64_t pa_fused_tuned_lds_bytes(int br, int bc, int double_buffer, int64_t d, int dtype);
 
-/* LDS bytes one workgroup of fused_tc needs, or -1 if (d, dtype) is not compiled.
+/* LDS bytes one workgroup of fused_tc needs, or -1 if (d, dtype) is not compiled: the largest of
+ * its launch forms (the persistent forms add rows that stage O before its stores).
  * Replaces fused_tc_smem_bytes (csrc/kernels/fused_tc.cuh:184). No GPU needed. */
 int64_t pa_fused_tc_lds_bytes(int64_t d, int dtype);
 
