@@ -574,6 +574,49 @@ def test_key_split_matches_unsplit(n, dtype, causal):
     assert max_err(small, big) <= tol
 
 
+def f64_rows_gpu(q, k, v, head, rows, causal):
+    """float64 softmax(QK^T/sqrt(d))V of one head's query rows `rows` (a 1-D index tensor), on
+    the GPU: scores of these rows against every key."""
+    d = q.shape[-1]
+    s = torch.matmul(q[0, head, rows].double(), k[0, head].double().T.contiguous()) / np.sqrt(d)
+    if causal:
+        keys = torch.arange(q.shape[2], device=q.device)
+        s.masked_fill_(keys[None, :] > rows[:, None], float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v[0, head].double())
+
+
+# Rows far longer than the configurations': one head stays below 2 GiB, so every offset inside the
+# kernels is 32-bit; 8 heads, so causal takes the persistent causal form (B*H a multiple of 8).
+LONG_ROWS = [  # (N, d, dtype)
+    (65536, 128, torch.bfloat16),
+    (131072, 64, torch.float16),
+]
+
+
+@pytest.mark.parametrize("n, d, dtype", LONG_ROWS)
+@pytest.mark.parametrize("causal", [False, True])
+def test_long_rows_match_float64(n, d, dtype, causal):
+    """The first, middle and last 64 query rows of heads 0 and 7 against float64, at 2e-3 (wider
+    only where the reference algorithm itself misses float64 by more: the first causal rows,
+    which average over a handful of keys)."""
+    q, k, v = make_qkv(1, 8, n, d, dtype, seed=33, device="cuda")
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    print(f"[long rows] N={n} d={d} {dtype} causal={causal}: "
+          f"{_native.fused_tc_kernel(code, _native.DTYPE_F32, 8, n, d, causal)}", flush=True)
+    out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 64), torch.arange(n // 2 - 32, n // 2 + 32), torch.arange(n - 64, n)]).cuda()
+    for head in (0, 7):
+        ref = f64_rows_gpu(q, k, v, head, rows, causal)
+        err = (out[0, head, rows].double() - ref).abs().max().item()
+        bar = 2e-3
+        if causal:
+            qn, kn, vn = (t[0, head:head + 1].float().cpu().numpy() for t in (q, k, v))
+            bar, e_ref, _ = pb.reference_bar(qn, kn, vn, True, dtype, ref[None, :64].cpu().numpy(), q_rows=(0, 64))
+        print(f"  head {head}: max abs error {err:.2e} (bar {bar:.1e})", flush=True)
+        assert err <= bar
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_c4_shape_causal_matches_float64(causal):
     """Causal at the headline bf16 / d=128 shape (4 heads): the path the non-causal bench skips.
