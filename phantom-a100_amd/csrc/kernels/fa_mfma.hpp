@@ -424,53 +424,73 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   };
 
   // O = O^T / l for the current block. Register r of block db holds dim 32*db + 8*(r/4) + 4*hi + r%4.
-  // Persistent forms: through the wave's LDS rows (16-byte chunks XOR-swizzled by row), then
-  // non-temporal 16-byte buffer stores that each cover whole rows. O is written once and not
-  // read again, and whole-row stores let the lines leave L2 during the kernel instead of with the
-  // cache writeback at its end (C3 +4 %; stores of the lane's 8-byte pieces, non-temporal or
-  // write-through, were 13-15 % slower). Rows past N fall outside the buffer and are dropped.
-  auto store_block = [&]() {
-    const float l_tot = lacc[0];
-    const float inv = 1.f / l_tot;
+  // Staged stores: each wave writes its 32 rows of O into LDS rows of its own (16-byte chunks
+  // XOR-swizzled by row) and reads them back as whole rows, for non-temporal 16-byte buffer stores
+  // that each cover whole rows. O is written once and not read again, and whole-row stores let the
+  // lines leave L2 during the kernel instead of with the cache writeback at its end (persistent C3
+  // +4 %, per-block launches at the C3 / C4 shapes +3 / +1.4 %; stores of the lane's 8-byte pieces,
+  // non-temporal or write-through, were 13-15 % slower). Rows past N fall outside the buffer and
+  // are dropped. The persistent forms stage in o_lds; the two-stage per-block forms, which end with
+  // their block, in the K/V stages: wave w in stage object w % 4 at slot w / 4. The key-split and
+  // single-stage forms store each lane's pieces directly (staged, C2 was 2 % slower, and the
+  // single-stage 128 x 32 tile lost a wave per SIMD).
+  constexpr bool PB_STAGED = !PERSIST && KSPLIT == 1 && STAGES == 2;
+  constexpr int PB_SLOT = L::TILE_BYTES / ((NW + 3) / 4);   // staging bytes per wave
+  constexpr int PB_ROWS = PB_SLOT >= 32 * OROW ? 32 : PB_SLOT >= 16 * OROW ? 16 : PB_SLOT >= 8 * OROW ? 8 : 4;
+  static_assert(!PB_STAGED || ((PB_ROWS * OCR) % kWave == 0 && PB_ROWS * OROW <= PB_SLOT),
+                "per-block O staging: whole wave reads");
+  auto store_rows = [&](unsigned char* ws, auto rows_c) {   // rows_c: rows per pass
+    constexpr int R = decltype(rows_c)::value;
+    constexpr int PASSES = 32 / R;
+    constexpr int kNonTemporal = 2;   // buffer store cache policy: nt
     typedef OutT OutV4 __attribute__((ext_vector_type(4)));
-    if constexpr (PERSIST) {
-      constexpr int kNonTemporal = 2;   // buffer store cache policy: nt
-      unsigned char* ws = o_lds + wave * ORW * OROW;
-      const rsrc_t o_rs = make_rsrc(O + base, (uint32_t)((size_t)N * OROW));
-      // Lane-derived offsets behind an empty asm: hoisted out of the block loop they cost ~14 VGPRs.
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-      // Chunk swizzle of a staged row: 128-byte rows (8 chunks) pair up rows as the K tiles do, so
-      // the 32 rows written at one chunk spread over all 64 banks; longer rows XOR by row % chunks.
-      auto o_swz = [](int row) { return OCR == 8 ? (row >> 1) & 7 : row % OCR; };
-      const int lq_ = ln % 32, hi_ = ln / 32;
+    const float inv = 1.f / lacc[0];
+    const rsrc_t o_rs = make_rsrc(O + base, (uint32_t)((size_t)N * OROW));
+    // Lane-derived offsets behind an empty asm: hoisted out of the block loop they cost ~14 VGPRs.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    // Chunk swizzle of a staged row: 128-byte rows (8 chunks) pair up rows as the K tiles do, so
+    // the 32 rows written at one chunk spread over all 64 banks; longer rows XOR by row % chunks.
+    auto o_swz = [](int row) { return OCR == 8 ? (row >> 1) & 7 : row % OCR; };
+    const int lq_ = ln % 32, hi_ = ln / 32;
 #pragma unroll
-      for (int p = 0; p < OPASS; ++p) {
-        if (lq_ / ORW == p) {
-          const int row = lq_ % ORW;
+    for (int p = 0; p < PASSES; ++p) {
+      if (lq_ / R == p) {
+        const int row = lq_ % R;
 #pragma unroll
-          for (int db = 0; db < NDB; ++db)
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              OutV4 w;
+          for (int g4 = 0; g4 < 4; ++g4) {
+            OutV4 w;
 #pragma unroll
-              for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);
-              const int byte = (32 * db + 8 * g4 + 4 * hi_) * (int)sizeof(OutT);
-              *reinterpret_cast<OutV4*>(ws + row * OROW + (((byte / 16) ^ o_swz(row)) * 16) + byte % 16) = w;
-            }
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's rows are in LDS
-#pragma unroll
-        for (int i = 0; i < ORW * OCR / kWave; ++i) {
-          const int c16 = i * kWave + ln, row = c16 / OCR, c = c16 % OCR;
-          const u32x4 d = *reinterpret_cast<const u32x4*>(ws + row * OROW + ((c ^ o_swz(row)) * 16));
-          // (fp32 O: a head can span up to 4 GiB, so the offset is unsigned.)
-          __builtin_amdgcn_raw_buffer_store_b128(d, o_rs, (uint32_t)(q0w + p * ORW + row) * (uint32_t)OROW + c * 16, 0,
-                                                 kNonTemporal);
-        }
-        if (p + 1 < OPASS) __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next pass
+            for (int rr = 0; rr < 4; ++rr) w[rr] = from_f32<OutT>(o[db][g4 * 4 + rr] * inv);
+            const int byte = (32 * db + 8 * g4 + 4 * hi_) * (int)sizeof(OutT);
+            *reinterpret_cast<OutV4*>(ws + row * OROW + (((byte / 16) ^ o_swz(row)) * 16) + byte % 16) = w;
+          }
       }
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's rows are in LDS
+#pragma unroll
+      for (int i = 0; i < R * OCR / kWave; ++i) {
+        const int c16 = i * kWave + ln, row = c16 / OCR, c = c16 % OCR;
+        const u32x4 d = *reinterpret_cast<const u32x4*>(ws + row * OROW + ((c ^ o_swz(row)) * 16));
+        // (fp32 O: a head can span up to 4 GiB, so the offset is unsigned.)
+        __builtin_amdgcn_raw_buffer_store_b128(d, o_rs, (uint32_t)(q0w + p * R + row) * (uint32_t)OROW + c * 16, 0,
+                                               kNonTemporal);
+      }
+      if (p + 1 < PASSES) __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next pass
+    }
+  };
+  auto store_block = [&]() {
+    if constexpr (PERSIST) {
+      store_rows(o_lds + wave * ORW * OROW, std::integral_constant<int, ORW>{});
+    } else if constexpr (PB_STAGED) {
+      __syncthreads();   // every wave is done with the K/V stages
+      const int obj = wave % 4;
+      unsigned char* st = obj == 0 ? k_lds0 : obj == 1 ? v_lds0 : obj == 2 ? k_lds1 : v_lds1;
+      store_rows(st + (wave / 4) * PB_SLOT, std::integral_constant<int, PB_ROWS>{});
     } else if (g == 0 && qrow < N) {
+      typedef OutT OutV4 __attribute__((ext_vector_type(4)));
+      const float inv = 1.f / lacc[0];
       OutT* orow = O + base + (size_t)qrow * D;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
