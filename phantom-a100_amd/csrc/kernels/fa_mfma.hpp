@@ -74,8 +74,8 @@
 //    take the fast path without a runtime test. RAGGED: the same walk for an even tile count
 //    whose last tile is partial, or an odd count of full tiles padded with one empty tile; both
 //    wrap iterations then take the generic path and mask the tiles past N.
-//  * CAUSAL (the persistent form for causal rows, N a multiple of BM, B*H a multiple of 8): a
-//    block of query rows [q0, q0 + BM) sees its c = q0 / BN first key tiles unmasked in every
+//  * CAUSAL (the persistent form for causal rows, N a multiple of BM; XCD x owns the heads x,
+//    x + 8, ...): a block of query rows [q0, q0 + BM) sees its c = q0 / BN first key tiles unmasked in every
 //    wave, and then BM / BN diagonal tiles, of which wave w needs the first w / 2 + 1 (the last
 //    one masked). The c clean tiles run the clean persistent iterations; the diagonal tiles (with
 //    the two before them) run copies (DIAG) in which each wave takes the fast path up to its last
@@ -210,17 +210,18 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // Query block blk = (head, BM-query block). The persistent form walks the blocks of its XCD's
   // range (blk = x * range + c + C * j for the c-th of the C workgroups on XCD x), so that all
   // blocks of a head still run on one XCD.
-  // CAUSAL: XCD x owns the heads x, x + 8, x + 16, ...; its list holds their blocks head by head,
-  // longest (last query block) first within a head. Step j of the c-th of the C workgroups takes
-  // list entry j * C + c for even j and j * C + C - 1 - c for odd j (serpentine), -1 past the end.
+  // CAUSAL: XCD x owns the heads x, x + 8, x + 16, ... below B*H; its list holds their blocks
+  // head by head, longest (last query block) first within a head. Step j of the c-th of the C
+  // workgroups takes list entry j * C + c for even j and j * C + C - 1 - c for odd j
+  // (serpentine), -1 past the end of its XCD's list.
   const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
   int blk = 0, blk_step = 0, blk_end = 0, walk = 0;
   auto causal_block = [&](int j) -> int {
-    const int wgs = (int)gridDim.x / kNumXcd, c = (int)blockIdx.x / kNumXcd;
-    const int entries = total_blocks / kNumXcd;   // the launcher guarantees B*H % 8 == 0
+    const int wgs = (int)gridDim.x / kNumXcd, c = (int)blockIdx.x / kNumXcd, x = (int)blockIdx.x % kNumXcd;
+    const int heads = (total_blocks / num_qblocks - x + kNumXcd - 1) / kNumXcd;   // of XCD x
     const int e = j * wgs + ((j & 1) ? wgs - 1 - c : c);
-    if (e >= entries) return -1;
-    const int head = (int)blockIdx.x % kNumXcd + kNumXcd * (e / num_qblocks);
+    if (e >= heads * num_qblocks) return -1;
+    const int head = x + kNumXcd * (e / num_qblocks);
     return head * num_qblocks + (num_qblocks - 1 - e % num_qblocks);
   };
   if constexpr (CAUSAL) {

@@ -103,17 +103,25 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
 // 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
 // C5 845 -> 890 (back to back), 605 -> 627 and 821 -> 859 under the flushing protocol.
-// Causal rows take the CAUSAL form when every query block is full (N a multiple of BM) and every
-// XCD can own whole heads (B*H a multiple of 8): its workgroups walk their XCD's heads round by
-// round, so each gets the same number of key tiles (the per-block launch leaves CUs idle between
-// blocks of unequal length and ends with the most loaded CU).
+// Causal rows take the CAUSAL form when every query block is full (N a multiple of BM) and the
+// XCDs, each owning whole heads, get about as many heads each (below): its workgroups walk their
+// XCD's heads round by round, so each gets the same number of key tiles (the per-block launch
+// leaves CUs idle between blocks of unequal length and ends with the most loaded CU).
 // (Only the two-stage fused_tc kernels without a key split have persistent forms; the caller,
 // persistent_grid_for, is instantiated for those alone.)
 bool persistent_launch(int64_t n, int bm, int bn, int64_t bh, int causal) {
   if (!persistent_enabled()) return false;
   // (An odd count of full tiles is padded with an empty one; a single tile is not, since a bf16
   // row of one tile takes its P as two terms, which only the per-block launch does.)
-  return causal ? (n % bm == 0 && bh % pa::kNumXcd == 0) : ((n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn));
+  // Causal: each XCD walks whole heads, so B*H not a multiple of 8 leaves some XCDs one head more;
+  // taken while that is at most 25 % above the mean (and, in persistent_grid_for, while every XCD
+  // has a block for each of its workgroups). Measured against the per-block launch, causal TFLOP/s:
+  // bf16 d = 128 N = 4096, B*H = 63 / 42 / 20: 961 -> 1182, 877 -> 931, 738 -> 886; B*H = 100,
+  // N = 1024: 485 -> 694; fp16 d = 64, B*H = 81, N = 2048: 558 -> 715. Outside the rule it lost:
+  // B*H = 12 (N = 4096, d = 128) 619 -> 601, fp16 d = 64 B*H = 42 N = 2048 (under one block per
+  // workgroup on every XCD, so a CU's three workgroups took blocks of one length) 453 -> 374.
+  const bool heads_even = (bh + pa::kNumXcd - 1) / pa::kNumXcd * pa::kNumXcd * 4 <= bh * 5;
+  return causal ? (n % bm == 0 && heads_even) : ((n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn));
 }
 // Workgroups of the persistent launch: wgs_per_cu per CU, at most as many per XCD as the XCD has
 // blocks.
@@ -150,7 +158,13 @@ int persistent_grid_for(int64_t n, int64_t bh, int causal) {
   static_assert(ST == 2 && KS == 1, "persistent forms: two stages, no key split");
   if (!persistent_launch(n, BM, BN, bh, causal)) return 0;
   const long long total = (n + BM - 1) / BM * bh;
-  if (causal) return persistent_grid(total, persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, true>());
+  if (causal) {
+    const int wpc = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, true>();
+    // B*H not a multiple of 8: every XCD needs at least one block per workgroup (its fewest heads).
+    if (bh % pa::kNumXcd != 0 && bh / pa::kNumXcd * (n / BM) < (long long)device_cus() / pa::kNumXcd * wpc)
+      return 0;
+    return persistent_grid(total, wpc);
+  }
   const int clean = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false>();
   if (n % (2 * BN) == 0) return persistent_grid(total, clean);
   const int ragged = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false>();

@@ -481,7 +481,8 @@ def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtyp
     assert err <= tol + out_ulp, f"max abs error {err:.3e} > {tol:.1e} (reference algorithm vs float64 {e_ref:.2e})"
 
 
-# The causal persistent form (N a multiple of the block's 256 / 128 queries, B*H a multiple of 8)
+# The causal persistent form (N a multiple of the block's 256 / 128 queries; B*H a multiple of 8 or
+# within the launcher's rule for uneven heads per XCD)
 # against the per-block launch, bit for bit: C4 and C3/C5 shapes made causal, one block per head
 # (every wave's only tiles are diagonal, two-term bf16 P on one-tile rows), a block count per head
 # that is not a power of two, rescaling rows, more blocks than workgroups, fp32 outputs.
@@ -498,6 +499,13 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((4, 64, 128), torch.bfloat16, 1.0, torch.float32, 64),
     ((2, 8, 384), torch.bfloat16, 3.0, None, 64),
     ((2, 8, 640), torch.float16, 10.0, torch.float32, 64),
+    # B*H not a multiple of 8 (some XCDs own one head more), at least one block per workgroup
+    ((1, 100, 1024), torch.bfloat16, 1.0, None, 128),
+    ((3, 27, 2048), torch.float16, 3.0, torch.float32, 64),
+    ((2, 45, 2048), torch.bfloat16, 1.0, torch.float32, 64),
+    ((1, 63, 2048), torch.bfloat16, 1.0, None, 128),
+    ((1, 42, 4096), torch.bfloat16, 1.0, torch.float32, 128),
+    ((1, 20, 8192), torch.float16, 1.0, None, 64),
 ]
 
 
@@ -591,6 +599,22 @@ LONG_ROWS = [  # (N, d, dtype)
     (65536, 128, torch.bfloat16),
     (131072, 64, torch.float16),
 ]
+
+
+@pytest.mark.parametrize("bh", [42, 12, 20])
+def test_causal_with_uneven_heads_per_xcd_takes_the_per_block_launch(bh):
+    """Causal B*H not a multiple of 8 whose whole heads per XCD would leave an XCD more than 25 %
+    above the mean (12), or some XCD with fewer blocks than workgroups (42 and 20 at N = 1024,
+    d = 128), keeps the per-block launch, and still matches float64."""
+    desc = _native.fused_tc_kernel(_native.DTYPE_BF16, _native.DTYPE_F32, bh, 1024, 128, True)
+    assert "persistent" not in desc, desc
+    q, k, v = make_qkv(1, bh, 1024, 128, torch.bfloat16, seed=9, device="cuda")
+    out = cuda_attn.fused_tc(q, k, v, True, out_dtype=torch.float32)
+    heads = [0, bh - 1]
+    ref = f64_reference_gpu(q[:, heads].contiguous(), k[:, heads].contiguous(), v[:, heads].contiguous(), True)
+    qn, kn, vn = (t[0, heads].float().cpu().numpy() for t in (q, k, v))
+    tol, _, _ = pb.reference_bar(qn, kn, vn, True, torch.bfloat16, ref[0, :, :64].cpu().numpy(), q_rows=(0, 64))
+    assert max_err(out[:, heads], ref) <= tol
 
 
 @pytest.mark.parametrize("n, d, dtype", LONG_ROWS)
