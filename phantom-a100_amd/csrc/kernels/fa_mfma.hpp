@@ -140,7 +140,8 @@ template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPL
 __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT)
 __attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, CAUSAL>())))
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
-            OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal) {
+            OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal,
+            int cus_per_xcd) {
   typedef typename vec8<T>::type V8;
   typedef MfmaLds<D, BN, STAGES> L;
   constexpr float kLazyLog2 = 8.f;       // P stays below 2^kLazyLog2 between rescales
@@ -211,15 +212,26 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // range (blk = x * range + c + C * j for the c-th of the C workgroups on XCD x), so that all
   // blocks of a head still run on one XCD.
   // CAUSAL: XCD x owns the heads x, x + 8, x + 16, ... below B*H; its list holds their blocks
-  // head by head, longest (last query block) first within a head. Step j of the c-th of the C
-  // workgroups takes list entry j * C + c for even j and j * C + C - 1 - c for odd j
-  // (serpentine), -1 past the end of its XCD's list.
+  // head by head, longest (last query block) first within a head. The list is dealt out in passes
+  // over the XCD's cus_per_xcd CUs: workgroup c of the XCD runs on its CU c % cus_per_xcd (the
+  // dispatcher places an XCD's workgroups on its CUs in turn) as slot c / cus_per_xcd, and step j
+  // of it takes pass p = j * slots + slot, entry p * cus_per_xcd + u for CU u in even passes and
+  // p * cus_per_xcd + cus_per_xcd - 1 - u in odd ones (serpentine), -1 past the end of the list.
+  // So the workgroups sharing a CU take blocks from opposite ends of the length order, and every
+  // CU gets about the same number of key tiles. Where the workgroups do not fill whole slots
+  // (cus_per_xcd 0, or fewer blocks than slots), the passes run over the workgroups instead.
   const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
   int blk = 0, blk_step = 0, blk_end = 0, walk = 0;
   auto causal_block = [&](int j) -> int {
     const int wgs = (int)gridDim.x / kNumXcd, c = (int)blockIdx.x / kNumXcd, x = (int)blockIdx.x % kNumXcd;
     const int heads = (total_blocks / num_qblocks - x + kNumXcd - 1) / kNumXcd;   // of XCD x
-    const int e = j * wgs + ((j & 1) ? wgs - 1 - c : c);
+    int e;
+    if (cus_per_xcd > 0 && wgs % cus_per_xcd == 0) {
+      const int u = c % cus_per_xcd, p = j * (wgs / cus_per_xcd) + c / cus_per_xcd;
+      e = p * cus_per_xcd + ((p & 1) ? cus_per_xcd - 1 - u : u);
+    } else {
+      e = j * wgs + ((j & 1) ? wgs - 1 - c : c);
+    }
     if (e >= heads * num_qblocks) return -1;
     const int head = x + kNumXcd * (e / num_qblocks);
     return head * num_qblocks + (num_qblocks - 1 - e % num_qblocks);

@@ -189,14 +189,15 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
                                           : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
         hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                           static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);
+                           static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal,
+                           device_cus() / pa::kNumXcd);
         return hipGetLastError();
       }
     }
   }
   hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS>), dim3((unsigned)total), dim3(BM / 32 * pa::kWave * KS), 0,
                      stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal);
+                     static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal, 0);
   return hipGetLastError();
 }
 
