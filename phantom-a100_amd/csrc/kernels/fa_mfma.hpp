@@ -517,6 +517,32 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     }
   };
 
+  // Two-stage prologue: the first tiles into LDS, all in flight together. The persistent forms
+  // (at least two tiles per block) load K(0), V(0) and K(1) and wait for Q, K(0) and V(0) only
+  // (vmcnt counts these loads in issue order), so the first tile's MFMAs run while K(1) arrives;
+  // the wait after the first tile covers it before iteration 0. Their V(1) comes with iteration 0.
+  // The per-block forms load K(0), V(0), K(1), V(1) and wait for all of them.
+  auto prologue_loads = [&]() {
+    if constexpr (PERSIST) {
+      load_tile(k_rs, k_src, k_stage(even), 0);
+      load_tile(v_rs, v_src, v_stage(even), 0);
+      load_tile(k_rs, k_src, k_stage(odd), BN);
+      __builtin_amdgcn_s_waitcnt(CPT);   // vmcnt(CPT) expcnt(0) lgkmcnt(0): all but K(1)
+    } else {
+      if (KSPLIT == 1 || tile_of(0) < ntiles) {   // a workgroup always has a first tile
+        load_tile(k_rs, k_src, k_stage(even), tile_of(0) * BN);
+        load_tile(v_rs, v_src, v_stage(even), tile_of(0) * BN);
+      }
+      if (tile_of(1) < ntiles) {
+        load_tile(k_rs, k_src, k_stage(odd), tile_of(1) * BN);
+        load_tile(v_rs, v_src, v_stage(odd), tile_of(1) * BN);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();
+  };
+  static_assert(CPT < 16, "prologue wait: vmcnt(CPT) in the low vmcnt bits");
+
   if constexpr (STAGES == 2 && std::is_same<T, bf16>::value) {
     // bf16: overflow check instead of a row max. The exponent's reference point is
     // m_ref = m + kShift, so the P.V operand is P' = 2^(S c - m_ref) = P 2^-kShift and
@@ -570,16 +596,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
 
     // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
     // for short rows); S(0).
-    if (KSPLIT == 1 || tile_of(0) < ntiles) {   // a workgroup always has a first tile
-      load_tile(k_rs, k_src, k_stage(even), tile_of(0) * BN);
-      load_tile(v_rs, v_src, v_stage(even), tile_of(0) * BN);
-    }
-    if (tile_of(1) < ntiles) {
-      load_tile(k_rs, k_src, k_stage(odd), tile_of(1) * BN);
-      load_tile(v_rs, v_src, v_stage(odd), tile_of(1) * BN);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    prologue_loads();
 
     // Score and P' buffers swap roles every iteration (the loop is unrolled by two so the swap
     // costs no register moves). On the fast path the first HALF P' registers of tile t and
@@ -604,7 +621,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       }
     };
     first_tile(sa, pa);
-    // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first.
+    // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first (and, in the
+    // persistent forms, K(1) must have landed).
+    if constexpr (PERSIST) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     // Persistent form: whether this workgroup has a next query block, and its index. The current
     // block's last two iterations (the "wrap" copies) load that block's K(0), K(1), V(0) and Q.
@@ -836,16 +855,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     // fp16: the row max of S(t+1) decides the rescale before its exponentials.
     // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
     // for short rows); S(0) and its row max.
-    if (KSPLIT == 1 || tile_of(0) < ntiles) {   // a workgroup always has a first tile
-      load_tile(k_rs, k_src, k_stage(even), tile_of(0) * BN);
-      load_tile(v_rs, v_src, v_stage(even), tile_of(0) * BN);
-    }
-    if (tile_of(1) < ntiles) {
-      load_tile(k_rs, k_src, k_stage(odd), tile_of(1) * BN);
-      load_tile(v_rs, v_src, v_stage(odd), tile_of(1) * BN);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    prologue_loads();
 
     // Two score buffers swap roles every iteration (the loop is unrolled by two so the swap
     // costs no register moves).
@@ -881,7 +891,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       }
     };
     first_tile(sa, pa);
-    // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first.
+    // Iteration 0 loads K(2) into K(0)'s stage: every wave must have read K(0) first (and, in the
+    // persistent forms, K(1) must have landed).
+    if constexpr (PERSIST) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     // Persistent form: the next query block of this workgroup, loaded by the wrap copies (as on
     // the bf16 path).
