@@ -594,8 +594,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     };
     constexpr int c0 = 0, ch = HALF, cf = PV_STEPS;
 
-    // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
-    // for short rows); S(0).
+    // Prologue: the first tiles into LDS together (one memory latency instead of two for short
+    // rows); S(0).
     prologue_loads();
 
     // Score and P' buffers swap roles every iteration (the loop is unrolled by two so the swap
@@ -853,8 +853,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     m_out = m_ref;
   } else if constexpr (STAGES == 2) {
     // fp16: the row max of S(t+1) decides the rescale before its exponentials.
-    // Prologue: K(0), V(0), K(1), V(1) into LDS together (one memory latency instead of two
-    // for short rows); S(0) and its row max.
+    // Prologue: the first tiles into LDS together (one memory latency instead of two for short
+    // rows); S(0) and its row max.
     prologue_loads();
 
     // Two score buffers swap roles every iteration (the loop is unrolled by two so the swap
