@@ -110,9 +110,25 @@ __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 // same XCD: the dispatcher sends workgroup g to XCD g % 8, so logical id
 // (g % 8) * (total / 8) + g / 8 keeps a contiguous range of (head, query-block) pairs - the
 // blocks that re-read the same K/V rows - inside one XCD's L2. Identity when total % 8 != 0.
-__device__ __forceinline__ int xcd_remap(int g, int total) {
+// (The launcher's model of the per-block launch evaluates it on the host.)
+__host__ __device__ __forceinline__ int xcd_remap(int g, int total) {
   if (total % kNumXcd != 0) return g;
   return (g % kNumXcd) * (total / kNumXcd) + g / kNumXcd;
+}
+
+// The causal walk's dealing: the entry of an XCD's block list taken at step j by workgroup c of
+// the XCD's wgs workgroups. Workgroup c runs on the XCD's CU u = c % cus_per_xcd (the dispatcher
+// places an XCD's workgroups on its CUs in turn) as slot c / cus_per_xcd; step j is pass
+// p = j * slots + slot of the list over the CUs, entry p * cus_per_xcd + u in even passes and
+// p * cus_per_xcd + cus_per_xcd - 1 - u in odd ones (serpentine). Where the workgroups do not
+// fill whole slots (cus_per_xcd 0, or fewer workgroups than the XCD has CUs times its slots), the
+// passes run over the workgroups instead. The launcher evaluates the same function on the host.
+__host__ __device__ __forceinline__ int causal_walk_entry(int j, int c, int wgs, int cus_per_xcd) {
+  if (cus_per_xcd > 0 && wgs % cus_per_xcd == 0) {
+    const int u = c % cus_per_xcd, p = j * (wgs / cus_per_xcd) + c / cus_per_xcd;
+    return p * cus_per_xcd + ((p & 1) ? cus_per_xcd - 1 - u : u);
+  }
+  return j * wgs + ((j & 1) ? wgs - 1 - c : c);
 }
 
 }  // namespace pa

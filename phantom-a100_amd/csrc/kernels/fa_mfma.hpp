@@ -74,10 +74,11 @@
 //    take the fast path without a runtime test. RAGGED: the same walk for an even tile count
 //    whose last tile is partial, or an odd count of full tiles padded with one empty tile; both
 //    wrap iterations then take the generic path and mask the tiles past N.
-//  * CAUSAL (the persistent form for causal rows, N a multiple of BM; XCD x owns the heads x,
-//    x + 8, ...): a block of query rows [q0, q0 + BM) sees its c = q0 / BN first key tiles unmasked in every
-//    wave, and then BM / BN diagonal tiles, of which wave w needs the first w / 2 + 1 (the last
-//    one masked). The c clean tiles run the clean persistent iterations; the diagonal tiles (with
+//  * CAUSAL (the persistent form for causal rows; XCD x owns the heads x, x + 8, ...): a block
+//    of query rows [q0, q0 + BM) sees its c = q0 / BN first key tiles unmasked in every wave, and
+//    then BM / BN diagonal tiles, of which wave w needs the first w / 2 + 1 (the last one masked).
+//    When N is not a multiple of BM, a head's last block holds the tiles up to N, padded to an
+//    even count; its waves need the tiles up to min(N, their last row + 1). The c clean tiles run the clean persistent iterations; the diagonal tiles (with
 //    the two before them) run copies (DIAG) in which each wave takes the fast path up to its last
 //    tile and idles after it, the fast path masking S(t+1) when t+1 is the wave's diagonal tile;
 //    only the block's very last tile (the last wrap copy) takes the generic path. Blocks are
@@ -124,21 +125,23 @@ template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 1
 // Minimum waves per SIMD the register allocator must allow (1: no constraint; PA_MFMA_MIN_WAVES
 // overrides it for every instantiation). Three 4-wave d = 64 workgroups per CU need at most 168
 // VGPRs: the fp16 causal persistent form takes 169 unconstrained, the bf16 non-causal persistent
-// forms 169-171 (held to 168 they spill 1-2 VGPRs and still run 3.5-6 % faster; the bf16 causal
-// form, at 193-195, stays at two).
+// forms 169-171 (held to 168 they spill 1-2 VGPRs and still run 3.5-6 % faster), the bf16 causal
+// form 193 (held to 168 it spills 10 VGPRs and runs 4-26 % faster: B*H x N = 256 x 512 404 -> 422,
+// 128 x 1024 516 -> 584, 128 x 2048 641 -> 794, 64 x 4096 692 -> 873, 16 x 8192 713 -> 887
+// TFLOP/s).
 #ifndef PA_MFMA_MIN_WAVES
 #define PA_MFMA_MIN_WAVES 0
 #endif
-template <typename T, int D, bool PERSIST, bool CAUSAL>
+template <typename T, int D, bool PERSIST, bool RAGGED, bool CAUSAL>
 constexpr int mfma_min_waves() {
   return PA_MFMA_MIN_WAVES > 0 ? PA_MFMA_MIN_WAVES
-                               : (PERSIST && D == 64 && (std::is_same<T, bf16>::value ? !CAUSAL : CAUSAL)) ? 3 : 1;
+                               : (PERSIST && D == 64 && (std::is_same<T, bf16>::value || RAGGED || CAUSAL)) ? 3 : 1;
 }
 
 template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false,
           bool RAGGED = false, bool CAUSAL = false>
 __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT)
-__attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, CAUSAL>())))
+__attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, RAGGED, CAUSAL>())))
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal,
             int cus_per_xcd) {
@@ -212,26 +215,16 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // range (blk = x * range + c + C * j for the c-th of the C workgroups on XCD x), so that all
   // blocks of a head still run on one XCD.
   // CAUSAL: XCD x owns the heads x, x + 8, x + 16, ... below B*H; its list holds their blocks
-  // head by head, longest (last query block) first within a head. The list is dealt out in passes
-  // over the XCD's cus_per_xcd CUs: workgroup c of the XCD runs on its CU c % cus_per_xcd (the
-  // dispatcher places an XCD's workgroups on its CUs in turn) as slot c / cus_per_xcd, and step j
-  // of it takes pass p = j * slots + slot, entry p * cus_per_xcd + u for CU u in even passes and
-  // p * cus_per_xcd + cus_per_xcd - 1 - u in odd ones (serpentine), -1 past the end of the list.
-  // So the workgroups sharing a CU take blocks from opposite ends of the length order, and every
-  // CU gets about the same number of key tiles. Where the workgroups do not fill whole slots
-  // (cus_per_xcd 0, or fewer blocks than slots), the passes run over the workgroups instead.
+  // head by head, longest (last query block) first within a head. The list is dealt out in
+  // serpentine passes over the XCD's cus_per_xcd CUs (causal_walk_entry), -1 past its end. So the
+  // workgroups sharing a CU take blocks from opposite ends of the length order, and where the
+  // blocks per head tile the passes evenly, every CU gets the same number of key tiles.
   const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
   int blk = 0, blk_step = 0, blk_end = 0, walk = 0;
   auto causal_block = [&](int j) -> int {
     const int wgs = (int)gridDim.x / kNumXcd, c = (int)blockIdx.x / kNumXcd, x = (int)blockIdx.x % kNumXcd;
     const int heads = (total_blocks / num_qblocks - x + kNumXcd - 1) / kNumXcd;   // of XCD x
-    int e;
-    if (cus_per_xcd > 0 && wgs % cus_per_xcd == 0) {
-      const int u = c % cus_per_xcd, p = j * (wgs / cus_per_xcd) + c / cus_per_xcd;
-      e = p * cus_per_xcd + ((p & 1) ? cus_per_xcd - 1 - u : u);
-    } else {
-      e = j * wgs + ((j & 1) ? wgs - 1 - c : c);
-    }
+    const int e = causal_walk_entry(j, c, wgs, cus_per_xcd);
     if (e >= heads * num_qblocks) return -1;
     const int head = x + kNumXcd * (e / num_qblocks);
     return head * num_qblocks + (num_qblocks - 1 - e % num_qblocks);
@@ -327,11 +320,14 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   const int wave_kv_end = causal ? min(kv_end, q0w + 32) : kv_end;  // keys this wave can see
   int wave_tiles = (wave_kv_end + BN - 1) / BN;
   // RAGGED with an odd tile count (every tile full): one more tile, entirely past N (it loads as
-  // zeros and is masked to P = 0), makes the count even for the wrap copies.
+  // zeros and is masked to P = 0), makes the count even for the wrap copies. CAUSAL: the same
+  // padding for a last query block that ends past N; the padded tile lies past every wave's last
+  // tile, so no wave computes on it.
   if constexpr (RAGGED) {
     ntiles += ntiles & 1;
     wave_tiles = ntiles;
   }
+  if constexpr (CAUSAL) ntiles += ntiles & 1;
   const int nit = (ntiles + KSPLIT - 1) / KSPLIT;   // iterations of every key group
   // Tiles [0, clean_tiles) need no mask for this wave: all keys < N and (causal) all keys at or
   // before the wave's first query.
@@ -359,8 +355,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     if constexpr (RAGGED) asm volatile("" : "+s"(j0));
     return j0;
   };
-  // CAUSAL form: the causal mask of the wave's diagonal tile (N is a multiple of BM there, so no
-  // key is past N). Key j0 + off (off = 32 b + 8 (r / 4) + 4 hi + r % 4) is visible iff
+  // CAUSAL form: the causal mask of the wave's diagonal tile (a key past N comes after every row
+  // before N, so this mask hides it too; rows past N, whose keys past N read as zeros, are never
+  // stored). Key j0 + off (off = 32 b + 8 (r / 4) + 4 hi + r % 4) is visible iff
   // 32 b + 8 (r / 4) + r % 4 <= qrow - j0 - 4 hi; that limit is hidden from the compiler, which
   // would otherwise hoist the 32 per-lane terms qrow - off out of the block loop (they spill).
   auto mask_diag = [&](f32x16 (&s)[NKB], int j0) {
@@ -795,7 +792,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     } else {
       // The launcher guarantees an even tile count nit = ntiles >= 2 in every block: the block's
       // last two iterations are the wrap copies. Non-causal: only the last tile can be partial
-      // (RAGGED), and the query block is blk % num_qblocks. CAUSAL: every query block is full.
+      // (RAGGED), and the query block is blk % num_qblocks. CAUSAL: only a head's last query
+      // block can end past N (its tile count padded to even).
       const std::true_type with_wrap{};
       const std::integral_constant<int, 2> diag{};
       const std::integral_constant<int, 3> diag_wrap{};
@@ -804,7 +802,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           blk_n = causal_block(walk + 1);
           has_next = blk_n >= 0;
           // Tiles [0, c) are clean in every wave; the per-wave copies start two tiles before c.
-          const int c = ntiles - BM / BN;
+          const int c = q0 / BN;
           for (int t = 0; t < c - 2; t += 2) {
             iteration(even, no_wrap, t, sa, sb, pa, pb);
             iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
@@ -833,7 +831,10 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         q0w = q0 + wave * 32;
         qrow = q0w + lq;
         if constexpr (CAUSAL) {
-          ntiles = (q0 + BM) / BN;
+          // (Not clamped at N: that differs only for a wave whose rows all lie past N, which
+          // computes on keys that read as zeros and stores nothing; the clamp costs 3 VGPRs and a
+          // spill in the bf16 d = 128 kernel. Every load and barrier is independent of wave_tiles.)
+          ntiles = (min(N, q0 + BM) + 2 * BN - 1) / (2 * BN) * 2;
           wave_tiles = (q0w + 32 + BN - 1) / BN;
         }
         base = (size_t)(blk / num_qblocks) * N * D;
@@ -1015,7 +1016,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           blk_n = causal_block(walk + 1);
           has_next = blk_n >= 0;
           // Tiles [0, c) are clean in every wave; the per-wave copies start two tiles before c.
-          const int c = ntiles - BM / BN;
+          const int c = q0 / BN;
           for (int t = 0; t < c - 2; t += 2) {
             iteration(even, no_wrap, t, sa, sb, pa, pb);
             iteration(odd, no_wrap, t + 1, sb, sa, pb, pa);
@@ -1044,7 +1045,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         q0w = q0 + wave * 32;
         qrow = q0w + lq;
         if constexpr (CAUSAL) {
-          ntiles = (q0 + BM) / BN;
+          ntiles = (min(N, q0 + BM) + 2 * BN - 1) / (2 * BN) * 2;
           wave_tiles = (q0w + 32 + BN - 1) / BN;
         }
         base = (size_t)(blk / num_qblocks) * N * D;

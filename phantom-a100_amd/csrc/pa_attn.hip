@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
+#include <vector>
 
 #include "phantom_attn.h"
 #include "kernels/fa_f32.hpp"
@@ -103,13 +104,13 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
 // 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
 // C5 845 -> 890 (back to back), 605 -> 627 and 821 -> 859 under the flushing protocol.
-// Causal rows take the CAUSAL form when every query block is full (N a multiple of BM) and the
-// XCDs, each owning whole heads, get about as many heads each (below): its workgroups walk their
-// XCD's heads round by round, so each gets the same number of key tiles (the per-block launch
+// Causal rows take the CAUSAL form when the XCDs, each owning whole heads, get about as many heads
+// each (below); N need not be a multiple of BM (a head's last block then ends past N, with rows
+// that are computed and not stored): its workgroups walk their XCD's heads round by round, so each gets the same number of key tiles (the per-block launch
 // leaves CUs idle between blocks of unequal length and ends with the most loaded CU).
 // (Only the two-stage fused_tc kernels without a key split have persistent forms; the caller,
 // persistent_grid_for, is instantiated for those alone.)
-bool persistent_launch(int64_t n, int bm, int bn, int64_t bh, int causal) {
+bool persistent_launch(int64_t n, int bn, int64_t bh, int causal) {
   if (!persistent_enabled()) return false;
   // (An odd count of full tiles is padded with an empty one; a single tile is not, since a bf16
   // row of one tile takes its P as two terms, which only the per-block launch does.)
@@ -121,7 +122,7 @@ bool persistent_launch(int64_t n, int bm, int bn, int64_t bh, int causal) {
   // B*H = 12 (N = 4096, d = 128) 619 -> 601, fp16 d = 64 B*H = 42 N = 2048 (under one block per
   // workgroup on every XCD, so a CU's three workgroups took blocks of one length) 453 -> 374.
   const bool heads_even = (bh + pa::kNumXcd - 1) / pa::kNumXcd * pa::kNumXcd * 4 <= bh * 5;
-  return causal ? (n % bm == 0 && heads_even) : ((n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn));
+  return causal ? heads_even : ((n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn));
 }
 // Workgroups of the persistent launch: wgs_per_cu per CU, at most as many per XCD as the XCD has
 // blocks.
@@ -130,16 +131,16 @@ int persistent_grid(long long total_blocks, int wgs_per_cu) {
   return (int)std::min<long long>((long long)device_cus() / pa::kNumXcd * wgs_per_cu, per_xcd) * pa::kNumXcd;
 }
 
-// Workgroups of the persistent kernel that fit on one CU of the current device (queried once per
-// device), 0 if unknown.
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool RAGGED, bool CAUSAL>
-int persistent_wgs_per_cu() {
+// Workgroups of an fa_mfma_fwd instantiation that fit on one CU of the current device (queried
+// once per device), 0 if unknown.
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool PERSIST, bool RAGGED, bool CAUSAL>
+int wgs_per_cu() {
   static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, RAGGED, CAUSAL>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, PERSIST, RAGGED, CAUSAL>,
                                                      BM / 32 * pa::kWave * KS, 0) != hipSuccess || n <= 0)
       return 0;
     cache[dev].store(n, std::memory_order_relaxed);
@@ -147,27 +148,128 @@ int persistent_wgs_per_cu() {
   return n;
 }
 
+// Causal rows: which launch finishes first, from a model of XCD 0 (it owns the most heads) under
+// each, in key tiles at one CU's rate, the rate of a CU being shared by the workgroups it holds.
+// The persistent launch ends with its busiest CU: each CU's tiles summed over the blocks the walk
+// (pa::causal_walk_entry) deals its workgroups. The per-block launch is simulated: its blocks in
+// dispatch order (workgroup g to XCD g % 8, block pa::xcd_remap(g)), each CU holding up to its
+// occupancy of them, a freed slot taking the next block on the CU that holds fewest. The walk's
+// serpentine passes pair every CU's long and short blocks when the blocks per head tile the
+// passes evenly (4 to 64 blocks per head at 32 CUs per XCD); other counts leave some CU well above
+// the mean, while the hardware dispatcher balances the per-block launch by itself (though it
+// dispatches head by head, longest block first, and can end with long blocks). The persistent
+// launch is taken while the model's per-block time is at least 0.85 of its own: on MI355X the
+// measured per-block / persistent time ratio was the model's times 0.9-1.25 (the persistent
+// launch also hides each block's start), e.g. model -> measured: bf16 d = 128 B*H = 32 N = 3072
+// 0.71 -> 0.87, B*H = 32 N = 6144 0.79 -> 0.94, B*H = 128 N = 768 0.83 -> 1.00, B*H = 128
+// N = 1536 0.93 -> 1.10, B*H = 42 N = 4096 0.97 -> 1.06, B*H = 128 N = 1000 1.40 -> 1.33;
+// fp16 d = 64 B*H = 128 N = 1030 0.73 -> 0.92, B*H = 16 N = 8000 0.83 -> 0.96, B*H = 42
+// N = 2048 0.84 -> 0.83, B*H = 32 N = 3072 0.84 -> 0.99, B*H = 16 N = 6144 0.85 -> 1.01,
+// B*H = 81 N = 2048 1.35 -> 1.28. The model runs once per shape (cached); beyond 64 blocks per
+// CU, where a pass's pattern averages out over many passes, the persistent launch is taken
+// without it.
+long long causal_block_tiles(long long qb, int64_t n, int bm, int bn) {
+  const long long t = (std::min<long long>(n, (qb + 1) * bm) + bn - 1) / bn;
+  return t + (t & 1);   // padded to even, as the kernel pads it
+}
+
+long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus) {
+  const long long nq = (n + bm - 1) / bm, heads = (bh + pa::kNumXcd - 1) / pa::kNumXcd;
+  std::vector<long long> load((size_t)cus, 0);
+  for (int c = 0; c < wgs; ++c) {
+    for (int j = 0;; ++j) {
+      const long long e = pa::causal_walk_entry(j, c, wgs, cus);
+      if (e >= heads * nq) break;
+      load[(size_t)(c % cus)] += causal_block_tiles(nq - 1 - e % nq, n, bm, bn);
+    }
+  }
+  return *std::max_element(load.begin(), load.end());
+}
+
+double per_block_makespan(int64_t n, int64_t bh, int bm, int bn, int slots, int cus) {
+  const long long nq = (n + bm - 1) / bm, total = nq * bh;
+  std::vector<double> done((size_t)cus, 0.0);          // work each resident block of a CU has had
+  std::vector<std::vector<double>> ends((size_t)cus);  // `done` at which each resident block ends
+  double now = 0.0;
+  long long g = 0;   // next workgroup id of XCD 0
+  while (true) {
+    while (g < total) {
+      size_t cu = 0;
+      for (size_t c = 1; c < ends.size(); ++c)
+        if (ends[c].size() < ends[cu].size()) cu = c;
+      if ((int)ends[cu].size() >= slots) break;
+      const long long blk = pa::xcd_remap((int)g, (int)total);
+      ends[cu].push_back(done[cu] + (double)causal_block_tiles(nq - 1 - blk % nq, n, bm, bn));
+      g += pa::kNumXcd;
+    }
+    double dt = 0.0;
+    bool any = false;
+    for (size_t c = 0; c < ends.size(); ++c) {
+      if (ends[c].empty()) continue;
+      const double left = (*std::min_element(ends[c].begin(), ends[c].end()) - done[c]) * (double)ends[c].size();
+      if (!any || left < dt) dt = left;
+      any = true;
+    }
+    if (!any) break;
+    now += dt;
+    for (size_t c = 0; c < ends.size(); ++c) {
+      if (ends[c].empty()) continue;
+      done[c] += dt / (double)ends[c].size();
+      const double at = done[c] + 1e-9 * (1.0 + done[c]);
+      ends[c].erase(std::remove_if(ends[c].begin(), ends[c].end(), [&](double e) { return e <= at; }), ends[c].end());
+    }
+  }
+  return now;
+}
+
+bool causal_persistent_pays(int64_t n, int64_t bh, int bm, int bn, int wgs, int slots, int cus) {
+  if (wgs <= 0 || slots <= 0 || cus <= 0) return false;
+  const long long heads = (bh + pa::kNumXcd - 1) / pa::kNumXcd;
+  if (heads * ((n + bm - 1) / bm) > 64LL * cus) return true;
+  struct Entry {
+    int64_t n = -1, bh = -1;
+    int bm = 0, wgs = 0, slots = 0, cus = 0;
+    bool pays = false;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  Entry& e = cache[(size_t)((uint64_t)(n * 1000003 + bh * 131 + bm + wgs) % 64)];
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (e.n == n && e.bh == bh && e.bm == bm && e.wgs == wgs && e.slots == slots && e.cus == cus) return e.pays;
+  }
+  const bool pays = per_block_makespan(n, bh, bm, bn, slots, cus) >=
+                    0.85 * (double)causal_walk_busiest(n, bh, bm, bn, wgs, cus);
+  std::lock_guard<std::mutex> lock(mu);
+  e.n = n; e.bh = bh; e.bm = bm; e.wgs = wgs; e.slots = slots; e.cus = cus; e.pays = pays;
+  return pays;
+}
+
 // Grid of the persistent launch of this call, 0 for one workgroup per query block. A call that
 // needs the RAGGED form keeps the persistent launch only if that kernel fits as many workgroups
-// per CU as the clean one: at d = 64 fp16 it needs 217 VGPRs (two workgroups per CU instead of
-// three), and there the per-block launch measured faster (4x16x4032 895 vs 864, 8x16x960 724 vs
-// 672 TFLOP/s), while at d = 128 (one workgroup per CU either way) padding an odd tile count
-// gained (bf16 4x32x4032 1190 -> 1221, 16x16x960 930 -> 960).
+// per CU as the clean one. It does at d = 128 (one workgroup per CU either way; padding an odd
+// tile count gained, bf16 4x32x4032 1190 -> 1221, 16x16x960 930 -> 960 TFLOP/s) and at d = 64,
+// where it is held to three (fp16 unconstrained took 217 VGPRs, two workgroups per CU, and lost
+// to the per-block launch: 4x16x4032 864 vs 895, 8x16x960 672 vs 724; held, with no spill, per
+// block -> persistent 4x16x4032 904 -> 905, 8x16x960 728 -> 720, 16x16x1000 775 -> 800,
+// 8x16x4050 908 -> 894, 1x16x8000 883 -> 920).
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
 int persistent_grid_for(int64_t n, int64_t bh, int causal) {
   static_assert(ST == 2 && KS == 1, "persistent forms: two stages, no key split");
-  if (!persistent_launch(n, BM, BN, bh, causal)) return 0;
+  if (!persistent_launch(n, BN, bh, causal)) return 0;
   const long long total = (n + BM - 1) / BM * bh;
   if (causal) {
-    const int wpc = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, true>();
+    const int wpc = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, true>();
     // B*H not a multiple of 8: every XCD needs at least one block per workgroup (its fewest heads).
-    if (bh % pa::kNumXcd != 0 && bh / pa::kNumXcd * (n / BM) < (long long)device_cus() / pa::kNumXcd * wpc)
+    if (bh % pa::kNumXcd != 0 && bh / pa::kNumXcd * ((n + BM - 1) / BM) < (long long)device_cus() / pa::kNumXcd * wpc)
       return 0;
-    return persistent_grid(total, wpc);
+    const int grid = persistent_grid(total, wpc);
+    const int per_block = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false, false>();
+    return causal_persistent_pays(n, bh, BM, BN, grid / pa::kNumXcd, per_block, device_cus() / pa::kNumXcd) ? grid : 0;
   }
-  const int clean = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false>();
+  const int clean = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, false>();
   if (n % (2 * BN) == 0) return persistent_grid(total, clean);
-  const int ragged = persistent_wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false>();
+  const int ragged = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, true, false>();
   return ragged >= clean ? persistent_grid(total, ragged) : 0;
 }
 

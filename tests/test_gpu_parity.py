@@ -436,20 +436,25 @@ PERSISTENT_SHAPES_D64 = [  # (B, H, N), dtype, qk_scale, out dtype; d = 64
     ((2, 16, 1000), torch.bfloat16, 1.0, torch.float32),
     ((4, 16, 4032), torch.bfloat16, 1.0, None),           # 63 full tiles, padded to 64
     ((1, 300, 192), torch.bfloat16, 3.0, torch.float32),  # three tiles, padded to four
+    ((4, 16, 4032), torch.float16, 1.0, None),            # fp16 RAGGED: 63 tiles, padded to 64
+    ((2, 16, 1000), torch.float16, 3.0, torch.float32),   # fp16 RAGGED: partial last tile
+    ((8, 16, 4050), torch.float16, 1.0, None),
 ]
 ALL_PERSISTENT = [(*c, 128) for c in PERSISTENT_SHAPES] + [(*c, 64) for c in PERSISTENT_SHAPES_D64]
 
 
-@pytest.mark.parametrize("n", [1000, 4032, 64])
-def test_fp16_d64_ragged_rows_take_the_per_block_launch(n):
-    """fp16 d = 64 rows that need the RAGGED form (a partial last tile, or an odd count of full
-    tiles) stay on the per-block launch: that kernel fits two workgroups per CU against the clean
-    persistent kernel's three, so the launcher keeps the per-block form, which is still correct."""
-    b, h = 2, 16
-    assert "persistent" in _native.fused_tc_kernel(_native.DTYPE_F16, _native.DTYPE_F16, b * h, 1024, 64)
-    desc = _native.fused_tc_kernel(_native.DTYPE_F16, _native.DTYPE_F16, b * h, n, 64)
+@pytest.mark.parametrize("n, d", [(64, 64), (40, 64), (64, 128), (33, 128)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_one_tile_rows_take_the_per_block_launch(n, d, dtype):
+    """Non-causal rows of one key tile are not padded to two (a bf16 row of one tile takes its P
+    as two terms, which only the per-block launch does): they take the per-block launch, on enough
+    heads for the persistent one otherwise, and still match float64."""
+    b, h = 8, 64
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    assert "persistent" in _native.fused_tc_kernel(code, code, b * h, 1024, d)
+    desc = _native.fused_tc_kernel(code, code, b * h, n, d)
     assert "persistent" not in desc, desc
-    q, k, v = make_qkv(b, h, n, 64, torch.float16, seed=7, device="cuda")
+    q, k, v = make_qkv(b, h, n, d, dtype, seed=7, device="cuda")
     out = cuda_attn.fused_tc(q, k, v, out_dtype=torch.float32)
     assert max_err(out, f64_reference_gpu(q, k, v)) <= 2e-3
 
@@ -481,11 +486,12 @@ def test_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtyp
     assert err <= tol + out_ulp, f"max abs error {err:.3e} > {tol:.1e} (reference algorithm vs float64 {e_ref:.2e})"
 
 
-# The causal persistent form (N a multiple of the block's 256 / 128 queries; B*H a multiple of 8 or
-# within the launcher's rule for uneven heads per XCD)
-# against the per-block launch, bit for bit: C4 and C3/C5 shapes made causal, one block per head
-# (every wave's only tiles are diagonal, two-term bf16 P on one-tile rows), a block count per head
-# that is not a power of two, rescaling rows, more blocks than workgroups, fp32 outputs.
+# The causal persistent form (B*H a multiple of 8 or within the launcher's rule for uneven heads
+# per XCD) against the per-block launch, bit for bit: C4 and C3/C5 shapes made causal, one block per
+# head (every wave's only tiles are diagonal, two-term bf16 P on one-tile rows), a block count per
+# head that is not a power of two, rescaling rows, more blocks than workgroups, fp32 outputs, and N
+# not a multiple of the block's 256 / 128 queries (a head's last block ends past N; its tile count
+# even, or odd and padded; N below one key tile).
 CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((4, 32, 4096), torch.bfloat16, 1.0, None, 128),
     ((4, 32, 4096), torch.float16, 1.0, None, 128),
@@ -506,6 +512,14 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((1, 63, 2048), torch.bfloat16, 1.0, None, 128),
     ((1, 42, 4096), torch.bfloat16, 1.0, torch.float32, 128),
     ((1, 20, 8192), torch.float16, 1.0, None, 64),
+    # N not a multiple of the query block
+    ((2, 8, 1000), torch.bfloat16, 1.0, None, 128),        # 16 tiles in the last block
+    ((1, 8, 300), torch.bfloat16, 10.0, torch.float32, 128),  # 5 tiles, padded to 6
+    ((1, 16, 20), torch.bfloat16, 1.0, torch.float32, 128),   # one partial tile, padded to 2
+    ((4, 8, 1030), torch.float16, 3.0, None, 64),           # 17 tiles, padded to 18
+    ((4, 64, 100), torch.bfloat16, 1.0, None, 64),
+    ((2, 8, 1000), torch.float16, 1.0, torch.float32, 64),
+    ((1, 42, 4000), torch.bfloat16, 1.0, torch.float32, 128),  # and uneven heads per XCD
 ]
 
 
@@ -534,6 +548,51 @@ def test_causal_persistent_form_matches_per_block_form(shape, dtype, qk_scale, o
     out_ulp = 0.5 * torch.finfo(got.dtype).eps * ref.abs().max().item()
     err = max_err(got.reshape(1, b * h, n, d)[:, heads], ref)
     assert err <= tol + out_ulp, f"max abs error {err:.3e} > {tol:.1e} (reference algorithm vs float64 {e_ref:.2e})"
+
+
+# Q/K/V/O at the front of allocations whose tails (past the last head's N rows) hold NaN: a load
+# past a head's rows must read zeros without touching memory (the buffer range check; the K/V tile
+# start goes in the load's scalar offset), and a store past them must not land. A load that read
+# the tail would put NaN into O through P.V (0 * NaN = NaN). The tails are longer than any tile a
+# launch reads past N, so every access stays inside the allocation either way.
+BOUNDS_CASES = [  # (B, H, N), dtype, d, causal, persistent launch
+    ((2, 8, 1000), torch.bfloat16, 128, False, True),   # RAGGED: partial last tile
+    ((2, 8, 4032), torch.bfloat16, 64, False, True),    # RAGGED: 63 full tiles, padded to 64
+    ((2, 8, 1000), torch.bfloat16, 128, True, True),    # causal persistent, last block past N
+    ((1, 8, 20), torch.bfloat16, 128, True, True),      # causal persistent, N below one tile
+    ((1, 8, 1030), torch.float16, 64, True, True),      # causal persistent, 17 tiles padded to 18
+    ((2, 8, 1000), torch.bfloat16, 128, True, False),   # per-block launch
+    ((2, 8, 1000), torch.float16, 64, False, False),
+]
+
+
+@pytest.mark.parametrize("shape, dtype, d, causal, persistent", BOUNDS_CASES)
+def test_accesses_past_the_rows_touch_no_memory(shape, dtype, d, causal, persistent, per_block_launch):
+    b, h, n = shape
+    print(f"[bounds] {shape} d={d} {dtype} causal={causal} persistent={persistent}", flush=True)
+    q, k, v = make_qkv(b, h, n, d, dtype, seed=47, device="cuda")
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    per_block_launch(persistent)
+    desc = _native.fused_tc_kernel(code, code, b * h, n, d, causal)
+    assert ("persistent" in desc) == persistent, desc
+    numel, tail = q.numel(), 256 * d
+
+    def poisoned(t):
+        buf = torch.full((numel + tail,), float("nan"), dtype=dtype, device="cuda")
+        buf[:numel].copy_(t.reshape(-1))
+        return buf
+
+    qp, kp, vp = poisoned(q), poisoned(k), poisoned(v)
+    op = torch.full((numel + tail,), float("nan"), dtype=dtype, device="cuda")
+    rc = _native.lib().pa_fused_tc_fwd(qp.data_ptr(), kp.data_ptr(), vp.data_ptr(), op.data_ptr(), code, code,
+                                       b * h, n, d, int(causal), torch.cuda.current_stream().cuda_stream)
+    _native.check(rc, "pa_fused_tc_fwd")
+    want = cuda_attn.fused_tc(q, k, v, causal)
+    torch.cuda.synchronize()
+    got = op[:numel].reshape(b, h, n, d)
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want)
+    assert torch.isnan(op[numel:]).all()
 
 
 @pytest.mark.parametrize("n", [1, 15, 63, 64, 65, 200, 1000])

@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 
 # (entry, shape, dtype, causal, kwargs); the first GRAPH_CASES also run under graph capture (the
 # unfused entries allocate their score workspace per call). The causal fused_tc cases take the
-# causal persistent launch (B*H a multiple of 8, N a multiple of the query block).
+# causal persistent launch (B*H a multiple of 8).
 CASES = [
     ("fused_tc", (2, 8, 512, 128), torch.bfloat16, False, {}),
     ("fused_tc", (2, 8, 1000, 64), torch.float16, False, {}),
