@@ -86,11 +86,12 @@ int pa_fused_tuned_fwd(const void* q, const void* k, const void* v, void* o,
 /* v4 fused_tc: QK^T and PV on MFMA (fp16/bf16 in, fp32 accumulate), online softmax between.
  * dtype: F16 or BF16; out_dtype: dtype or F32; d in {64, 128}.
  * The launch is persistent (as many workgroups as fit on the device at once, walking the query
- * blocks) for causal == 0 with an even number of 64-key tiles, and for causal != 0 with n a
- * multiple of the query block (256 at d == 128, 128 at d == 64) and bh a multiple of 8 (or within
- * 25 % of an even split of whole heads over the 8 XCDs, with a query block for every workgroup),
- * unless pa_set_persistent(0) switched that off (see below); otherwise one workgroup per query
- * block.
+ * blocks) for causal == 0 with an even number of 64-key tiles (or an odd number, above one, of
+ * full ones), and for causal != 0 with bh a multiple of 8 (or within 25 % of an even split of
+ * whole heads over the 8 XCDs, with a query block for every workgroup) where a model of both
+ * launches (the walk's tiles per CU against the hardware's dispatch of one workgroup per query
+ * block) does not find the per-block launch faster; unless pa_set_persistent(0) switched that off
+ * (see below). Otherwise one workgroup per query block. pa_fused_tc_kernel names the choice.
  * Both launches give the same bits.
  * Replaces attn::launch_fused_tc (csrc/kernels/fused_tc.cuh:187-196) and fused_tc_forward
  * (csrc/attn_fused_tc.cu:5-19). */
