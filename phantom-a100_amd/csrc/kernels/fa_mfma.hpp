@@ -144,7 +144,7 @@ __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT)
 __attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, RAGGED, CAUSAL>())))
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal,
-            int cus_per_xcd) {
+            int cus_per_xcd, int walk_by_rank) {
   typedef typename vec8<T>::type V8;
   typedef MfmaLds<D, BN, STAGES> L;
   constexpr float kLazyLog2 = 8.f;       // P stays below 2^kLazyLog2 between rescales
@@ -215,19 +215,14 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // range (blk = x * range + c + C * j for the c-th of the C workgroups on XCD x), so that all
   // blocks of a head still run on one XCD.
   // CAUSAL: XCD x owns the heads x, x + 8, x + 16, ... below B*H; its list holds their blocks
-  // head by head, longest (last query block) first within a head. The list is dealt out in
-  // serpentine passes over the XCD's cus_per_xcd CUs (causal_walk_entry), -1 past its end. So the
-  // workgroups sharing a CU take blocks from opposite ends of the length order, and where the
-  // blocks per head tile the passes evenly, every CU gets the same number of key tiles.
+  // head by head, or by length when walk_by_rank is set, and is dealt out in serpentine passes
+  // over the XCD's cus_per_xcd CUs (causal_walk_block), so the workgroups sharing a CU take blocks
+  // from opposite ends of the length order.
   const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
   int blk = 0, blk_step = 0, blk_end = 0, walk = 0;
   auto causal_block = [&](int j) -> int {
-    const int wgs = (int)gridDim.x / kNumXcd, c = (int)blockIdx.x / kNumXcd, x = (int)blockIdx.x % kNumXcd;
-    const int heads = (total_blocks / num_qblocks - x + kNumXcd - 1) / kNumXcd;   // of XCD x
-    const int e = causal_walk_entry(j, c, wgs, cus_per_xcd);
-    if (e >= heads * num_qblocks) return -1;
-    const int head = x + kNumXcd * (e / num_qblocks);
-    return head * num_qblocks + (num_qblocks - 1 - e % num_qblocks);
+    return causal_walk_block(j, (int)blockIdx.x / kNumXcd, (int)blockIdx.x % kNumXcd, (int)gridDim.x / kNumXcd,
+                             cus_per_xcd, total_blocks / num_qblocks, num_qblocks, walk_by_rank);
   };
   if constexpr (CAUSAL) {
     blk = causal_block(0);

@@ -148,39 +148,44 @@ int wgs_per_cu() {
   return n;
 }
 
-// Causal rows: which launch finishes first, from a model of XCD 0 (it owns the most heads) under
-// each, in key tiles at one CU's rate, the rate of a CU being shared by the workgroups it holds.
+// Causal rows: which walk and which launch finish first, from a model of XCD 0 (it owns the most
+// heads), in key tiles at one CU's rate, the rate of a CU being shared by the workgroups it holds.
 // The persistent launch ends with its busiest CU: each CU's tiles summed over the blocks the walk
-// (pa::causal_walk_entry) deals its workgroups. The per-block launch is simulated: its blocks in
+// (pa::causal_walk_block) deals its workgroups. The per-block launch is simulated: its blocks in
 // dispatch order (workgroup g to XCD g % 8, block pa::xcd_remap(g)), each CU holding up to its
-// occupancy of them, a freed slot taking the next block on the CU that holds fewest. The walk's
-// serpentine passes pair every CU's long and short blocks when the blocks per head tile the
-// passes evenly (4 to 64 blocks per head at 32 CUs per XCD); other counts leave some CU well above
-// the mean, while the hardware dispatcher balances the per-block launch by itself (though it
-// dispatches head by head, longest block first, and can end with long blocks). The persistent
-// launch is taken while the model's per-block time is at least 0.85 of its own: on MI355X the
-// measured per-block / persistent time ratio was the model's times 0.9-1.25 (the persistent
-// launch also hides each block's start), e.g. model -> measured: bf16 d = 128 B*H = 32 N = 3072
-// 0.71 -> 0.87, B*H = 32 N = 6144 0.79 -> 0.94, B*H = 128 N = 768 0.83 -> 1.00, B*H = 128
-// N = 1536 0.93 -> 1.10, B*H = 42 N = 4096 0.97 -> 1.06, B*H = 128 N = 1000 1.40 -> 1.33;
-// fp16 d = 64 B*H = 128 N = 1030 0.73 -> 0.92, B*H = 16 N = 8000 0.83 -> 0.96, B*H = 42
-// N = 2048 0.84 -> 0.83, B*H = 32 N = 3072 0.84 -> 0.99, B*H = 16 N = 6144 0.85 -> 1.01,
-// B*H = 81 N = 2048 1.35 -> 1.28. The model runs once per shape (cached); beyond 64 blocks per
-// CU, where a pass's pattern averages out over many passes, the persistent launch is taken
-// without it.
+// occupancy of them, a freed slot taking the next block on the CU that holds fewest.
+// The walk's list runs head by head or by length. Head by head, the serpentine passes pair every
+// CU's long and short blocks only when the blocks per head tile the passes (4 to 64 blocks per head
+// at 32 CUs per XCD); other counts leave some CU 1.4-2.2x above the mean. By length, the passes
+// deal a sorted list and the busiest CU stays within ~10 % of the bound for any count. Measured on
+// MI355X (TFLOP/s, head by head -> by length, bitwise equal): d = 128 where head by head balances,
+// bf16 4x32x4096 1157 -> 1124, 2x16x8192 1236 -> 1233, 4x32x1024 836 -> 812 (the blocks at once
+// on an XCD share fewer heads' K/V in its L2), and B*H = 100 N = 1024 720 -> 677 (equal busiest
+// CUs); where it does not, bf16 4x32x1536 829 -> 938, 2x16x3072 783 -> 998, 1x32x6144 1041 -> 1150,
+// 1x42x4096 938 -> 1015. At d = 64 (three workgroups per CU) by length was faster everywhere:
+// fp16 8x16x1024 644 -> 682, 1x16x8192 840 -> 890, 8x16x1030 461 -> 584, 1x16x8000 696 -> 884,
+// 4x16x1536 572 -> 732, 2x16x3072 602 -> 792, 1x16x6144 694 -> 823. So d = 64 walks by length, and
+// d = 128 by length only where the model's busiest CU is lower that way.
+// The persistent launch is then taken while the model's per-block time is at least 0.85 of the
+// persistent one: the measured per-block / persistent time ratio ran at the model's times 0.9-1.25
+// (the persistent launch also hides each block's start); e.g. head by head, model -> measured,
+// bf16 d = 128 B*H = 32 N = 3072 0.71 -> 0.87, B*H = 128 N = 768 0.83 -> 1.00, B*H = 128 N = 1000
+// 1.40 -> 1.33, fp16 d = 64 B*H = 128 N = 1030 0.73 -> 0.92, B*H = 81 N = 2048 1.35 -> 1.28. The
+// model runs once per shape (cached); beyond 64 blocks per CU, where a pass's pattern averages out
+// over many passes, the persistent launch is taken without it.
 long long causal_block_tiles(long long qb, int64_t n, int bm, int bn) {
   const long long t = (std::min<long long>(n, (qb + 1) * bm) + bn - 1) / bn;
   return t + (t & 1);   // padded to even, as the kernel pads it
 }
 
-long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus) {
-  const long long nq = (n + bm - 1) / bm, heads = (bh + pa::kNumXcd - 1) / pa::kNumXcd;
+long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus, int by_rank) {
+  const int nq = (int)((n + bm - 1) / bm);
   std::vector<long long> load((size_t)cus, 0);
   for (int c = 0; c < wgs; ++c) {
     for (int j = 0;; ++j) {
-      const long long e = pa::causal_walk_entry(j, c, wgs, cus);
-      if (e >= heads * nq) break;
-      load[(size_t)(c % cus)] += causal_block_tiles(nq - 1 - e % nq, n, bm, bn);
+      const int blk = pa::causal_walk_block(j, c, 0, wgs, cus, (int)bh, nq, by_rank);
+      if (blk < 0) break;
+      load[(size_t)(c % cus)] += causal_block_tiles(blk % nq, n, bm, bn);
     }
   }
   return *std::max_element(load.begin(), load.end());
@@ -222,27 +227,38 @@ double per_block_makespan(int64_t n, int64_t bh, int bm, int bn, int slots, int 
   return now;
 }
 
-bool causal_persistent_pays(int64_t n, int64_t bh, int bm, int bn, int wgs, int slots, int cus) {
-  if (wgs <= 0 || slots <= 0 || cus <= 0) return false;
+struct CausalChoice {
+  bool persistent = false;
+  int by_rank = 0;
+};
+CausalChoice causal_choice(int64_t n, int64_t bh, int bm, int bn, int wgs, int slots, int cus, bool rank_only) {
+  if (wgs <= 0 || slots <= 0 || cus <= 0) return {};
   const long long heads = (bh + pa::kNumXcd - 1) / pa::kNumXcd;
-  if (heads * ((n + bm - 1) / bm) > 64LL * cus) return true;
+  if (heads * ((n + bm - 1) / bm) > 64LL * cus) return {true, rank_only ? 1 : 0};
   struct Entry {
     int64_t n = -1, bh = -1;
     int bm = 0, wgs = 0, slots = 0, cus = 0;
-    bool pays = false;
+    bool rank_only = false;
+    CausalChoice choice;
   };
   static std::mutex mu;
   static Entry cache[64];
   Entry& e = cache[(size_t)((uint64_t)(n * 1000003 + bh * 131 + bm + wgs) % 64)];
   {
     std::lock_guard<std::mutex> lock(mu);
-    if (e.n == n && e.bh == bh && e.bm == bm && e.wgs == wgs && e.slots == slots && e.cus == cus) return e.pays;
+    if (e.n == n && e.bh == bh && e.bm == bm && e.wgs == wgs && e.slots == slots && e.cus == cus &&
+        e.rank_only == rank_only)
+      return e.choice;
   }
-  const bool pays = per_block_makespan(n, bh, bm, bn, slots, cus) >=
-                    0.85 * (double)causal_walk_busiest(n, bh, bm, bn, wgs, cus);
+  const long long by_rank = causal_walk_busiest(n, bh, bm, bn, wgs, cus, 1);
+  const long long by_head = rank_only ? by_rank + 1 : causal_walk_busiest(n, bh, bm, bn, wgs, cus, 0);
+  CausalChoice choice;
+  choice.by_rank = by_rank < by_head ? 1 : 0;
+  choice.persistent = per_block_makespan(n, bh, bm, bn, slots, cus) >= 0.85 * (double)std::min(by_rank, by_head);
   std::lock_guard<std::mutex> lock(mu);
-  e.n = n; e.bh = bh; e.bm = bm; e.wgs = wgs; e.slots = slots; e.cus = cus; e.pays = pays;
-  return pays;
+  e.n = n; e.bh = bh; e.bm = bm; e.wgs = wgs; e.slots = slots; e.cus = cus; e.rank_only = rank_only;
+  e.choice = choice;
+  return choice;
 }
 
 // Grid of the persistent launch of this call, 0 for one workgroup per query block. A call that
@@ -253,24 +269,29 @@ bool causal_persistent_pays(int64_t n, int64_t bh, int bm, int bn, int wgs, int 
 // to the per-block launch: 4x16x4032 864 vs 895, 8x16x960 672 vs 724; held, with no spill, per
 // block -> persistent 4x16x4032 904 -> 905, 8x16x960 728 -> 720, 16x16x1000 775 -> 800,
 // 8x16x4050 908 -> 894, 1x16x8000 883 -> 920).
+struct PersistentPlan {
+  int grid = 0;      // workgroups of the persistent launch, 0 for one workgroup per query block
+  int by_rank = 0;   // causal walk: blocks by length rather than head by head
+};
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
-int persistent_grid_for(int64_t n, int64_t bh, int causal) {
+PersistentPlan persistent_grid_for(int64_t n, int64_t bh, int causal) {
   static_assert(ST == 2 && KS == 1, "persistent forms: two stages, no key split");
-  if (!persistent_launch(n, BN, bh, causal)) return 0;
+  if (!persistent_launch(n, BN, bh, causal)) return {};
   const long long total = (n + BM - 1) / BM * bh;
   if (causal) {
     const int wpc = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, true>();
     // B*H not a multiple of 8: every XCD needs at least one block per workgroup (its fewest heads).
     if (bh % pa::kNumXcd != 0 && bh / pa::kNumXcd * ((n + BM - 1) / BM) < (long long)device_cus() / pa::kNumXcd * wpc)
-      return 0;
+      return {};
     const int grid = persistent_grid(total, wpc);
     const int per_block = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false, false>();
-    return causal_persistent_pays(n, bh, BM, BN, grid / pa::kNumXcd, per_block, device_cus() / pa::kNumXcd) ? grid : 0;
+    const CausalChoice c = causal_choice(n, bh, BM, BN, grid / pa::kNumXcd, per_block, device_cus() / pa::kNumXcd, D == 64);
+    return c.persistent ? PersistentPlan{grid, c.by_rank} : PersistentPlan{};
   }
   const int clean = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, false>();
-  if (n % (2 * BN) == 0) return persistent_grid(total, clean);
+  if (n % (2 * BN) == 0) return {persistent_grid(total, clean), 0};
   const int ragged = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, true, false>();
-  return ragged >= clean ? persistent_grid(total, ragged) : 0;
+  return ragged >= clean ? PersistentPlan{persistent_grid(total, ragged), 0} : PersistentPlan{};
 }
 
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
@@ -281,25 +302,25 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
   if constexpr (TC && ST == 2 && KS == 1) {
     {
-      const int grid = persistent_grid_for<T, D, BM, BN, ST, OutT, KS>(n, bh, causal);
-      if (grid > 0) {
+      const PersistentPlan plan = persistent_grid_for<T, D, BM, BN, ST, OutT, KS>(n, bh, causal);
+      if (plan.grid > 0) {
         // Non-causal with N a multiple of 2 * BN: an even number of full tiles. Otherwise (an
         // even tile count whose last tile is partial, or an odd count of full tiles, padded with
         // an empty one) the RAGGED form, whose wrap copies mask the keys past N.
         auto kernel = causal ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false, true>
                       : n % (2 * BN) == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>
                                           : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
-        hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
+        hipLaunchKernelGGL(kernel, dim3((unsigned)plan.grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                            static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal,
-                           device_cus() / pa::kNumXcd);
+                           device_cus() / pa::kNumXcd, plan.by_rank);
         return hipGetLastError();
       }
     }
   }
   hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS>), dim3((unsigned)total), dim3(BM / 32 * pa::kWave * KS), 0,
                      stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal, 0);
+                     static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal, 0, 0);
   return hipGetLastError();
 }
 
@@ -310,7 +331,7 @@ struct MfmaEntry {
   mfma_fn fn;
   int64_t lds;
   bool tc;                 // fused_tc entry: may take the persistent launch
-  int (*persistent_grid)(int64_t n, int64_t bh, int causal);   // its persistent grid (tc entries)
+  PersistentPlan (*persistent_grid)(int64_t n, int64_t bh, int causal);   // its persistent launch (tc entries)
 };
 
 template <typename T> constexpr int dt_code();
@@ -319,7 +340,7 @@ template <> constexpr int dt_code<pa::bf16>() { return PA_DTYPE_BF16; }
 template <> constexpr int dt_code<float>() { return PA_DTYPE_F32; }
 
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool TC>
-constexpr int (*persistent_grid_fn())(int64_t, int64_t, int) {
+constexpr PersistentPlan (*persistent_grid_fn())(int64_t, int64_t, int) {
   if constexpr (TC && ST == 2 && KS == 1) return &persistent_grid_for<T, D, BM, BN, ST, OutT, KS>;
   else return nullptr;
 }
@@ -631,13 +652,13 @@ const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, 
   if (!e) return "";
   static const char* dt_name[] = {"f32", "f16", "bf16"};
   const long long total = (n + e->br - 1) / e->br * bh;
-  const int pgrid = e->persistent_grid ? e->persistent_grid(n, bh, causal) : 0;
-  const bool pers = pgrid > 0;   // as in launch_mfma: no device (grid 0) means one workgroup per block
+  const PersistentPlan plan = e->persistent_grid ? e->persistent_grid(n, bh, causal) : PersistentPlan{};
+  const bool pers = plan.grid > 0;   // as in launch_mfma: no device (grid 0) means one workgroup per block
   snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s> grid %d x %d threads",
            dt_name[e->dtype], e->d, e->br, e->bc, e->db ? 2 : 1, dt_name[e->out_dtype],
            e->ks == 2 ? ", key split 2" : "", pers ? ", persistent" : "",
-           !pers ? "" : causal ? ", causal" : n % (2 * e->bc) ? ", ragged" : "",
-           pers ? pgrid : (int)total, e->br / 32 * pa::kWave * e->ks);
+           !pers ? "" : causal ? (plan.by_rank ? ", causal, by rank" : ", causal") : n % (2 * e->bc) ? ", ragged" : "",
+           pers ? plan.grid : (int)total, e->br / 32 * pa::kWave * e->ks);
   return desc;
 }
 

@@ -520,7 +520,28 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((4, 64, 100), torch.bfloat16, 1.0, None, 64),
     ((2, 8, 1000), torch.float16, 1.0, torch.float32, 64),
     ((1, 42, 4000), torch.bfloat16, 1.0, torch.float32, 128),  # and uneven heads per XCD
+    # d = 128 walks by length where head by head leaves some CU above the others
+    ((2, 16, 3072), torch.bfloat16, 1.0, None, 128),
+    ((4, 32, 1536), torch.float16, 3.0, torch.float32, 128),
 ]
+
+# (B*H, N, d) -> the causal walk's order: head by head, or by length ("by rank").
+CAUSAL_WALKS = [
+    ((128, 4096, 128), False),   # 16 blocks per head tile the passes
+    ((32, 8192, 128), False),
+    ((32, 3072, 128), True),     # 12 blocks per head do not
+    ((128, 1536, 128), True),
+    ((128, 1024, 64), True),     # d = 64 always by length
+    ((16, 8000, 64), True),
+]
+
+
+@pytest.mark.parametrize("shape, by_rank", CAUSAL_WALKS)
+def test_causal_walk_order(shape, by_rank):
+    bh, n, d = shape
+    desc = _native.fused_tc_kernel(_native.DTYPE_BF16, _native.DTYPE_BF16, bh, n, d, True)
+    assert "persistent, causal" in desc, desc
+    assert ("by rank" in desc) == by_rank, desc
 
 
 @pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype, d", CAUSAL_PERSISTENT_SHAPES)
