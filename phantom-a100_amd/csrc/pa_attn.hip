@@ -22,6 +22,7 @@
 #include "kernels/fa_f32.hpp"
 #include "kernels/fa_mfma.hpp"
 #include "kernels/unfused.hpp"
+#include "launch_model.hpp"
 
 #ifndef PA_VERSION_STRING
 #define PA_VERSION_STRING "0.1.0"
@@ -148,119 +149,6 @@ int wgs_per_cu() {
   return n;
 }
 
-// Causal rows: which walk and which launch finish first, from a model of XCD 0 (it owns the most
-// heads), in key tiles at one CU's rate, the rate of a CU being shared by the workgroups it holds.
-// The persistent launch ends with its busiest CU: each CU's tiles summed over the blocks the walk
-// (pa::causal_walk_block) deals its workgroups. The per-block launch is simulated: its blocks in
-// dispatch order (workgroup g to XCD g % 8, block pa::xcd_remap(g)), each CU holding up to its
-// occupancy of them, a freed slot taking the next block on the CU that holds fewest.
-// The walk's list runs head by head or by length. Head by head, the serpentine passes pair every
-// CU's long and short blocks only when the blocks per head tile the passes (4 to 64 blocks per head
-// at 32 CUs per XCD); other counts leave some CU 1.4-2.2x above the mean. By length, the passes
-// deal a sorted list and the busiest CU stays within ~10 % of the bound for any count. Measured on
-// MI355X (TFLOP/s, head by head -> by length, bitwise equal): d = 128 where head by head balances,
-// bf16 4x32x4096 1157 -> 1124, 2x16x8192 1236 -> 1233, 4x32x1024 836 -> 812 (the blocks at once
-// on an XCD share fewer heads' K/V in its L2), and B*H = 100 N = 1024 720 -> 677 (equal busiest
-// CUs); where it does not, bf16 4x32x1536 829 -> 938, 2x16x3072 783 -> 998, 1x32x6144 1041 -> 1150,
-// 1x42x4096 938 -> 1015. At d = 64 (three workgroups per CU) by length was faster everywhere:
-// fp16 8x16x1024 644 -> 682, 1x16x8192 840 -> 890, 8x16x1030 461 -> 584, 1x16x8000 696 -> 884,
-// 4x16x1536 572 -> 732, 2x16x3072 602 -> 792, 1x16x6144 694 -> 823. So d = 64 walks by length, and
-// d = 128 by length only where the model's busiest CU is lower that way.
-// The persistent launch is then taken while the model's per-block time is at least 0.85 of the
-// persistent one: the measured per-block / persistent time ratio ran at the model's times 0.9-1.25
-// (the persistent launch also hides each block's start); e.g. head by head, model -> measured,
-// bf16 d = 128 B*H = 32 N = 3072 0.71 -> 0.87, B*H = 128 N = 768 0.83 -> 1.00, B*H = 128 N = 1000
-// 1.40 -> 1.33, fp16 d = 64 B*H = 128 N = 1030 0.73 -> 0.92, B*H = 81 N = 2048 1.35 -> 1.28. The
-// model runs once per shape (cached); beyond 64 blocks per CU, where a pass's pattern averages out
-// over many passes, the persistent launch is taken without it.
-long long causal_block_tiles(long long qb, int64_t n, int bm, int bn) {
-  const long long t = (std::min<long long>(n, (qb + 1) * bm) + bn - 1) / bn;
-  return t + (t & 1);   // padded to even, as the kernel pads it
-}
-
-long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus, int by_rank) {
-  const int nq = (int)((n + bm - 1) / bm);
-  std::vector<long long> load((size_t)cus, 0);
-  for (int c = 0; c < wgs; ++c) {
-    for (int j = 0;; ++j) {
-      const int blk = pa::causal_walk_block(j, c, 0, wgs, cus, (int)bh, nq, by_rank);
-      if (blk < 0) break;
-      load[(size_t)(c % cus)] += causal_block_tiles(blk % nq, n, bm, bn);
-    }
-  }
-  return *std::max_element(load.begin(), load.end());
-}
-
-double per_block_makespan(int64_t n, int64_t bh, int bm, int bn, int slots, int cus) {
-  const long long nq = (n + bm - 1) / bm, total = nq * bh;
-  std::vector<double> done((size_t)cus, 0.0);          // work each resident block of a CU has had
-  std::vector<std::vector<double>> ends((size_t)cus);  // `done` at which each resident block ends
-  double now = 0.0;
-  long long g = 0;   // next workgroup id of XCD 0
-  while (true) {
-    while (g < total) {
-      size_t cu = 0;
-      for (size_t c = 1; c < ends.size(); ++c)
-        if (ends[c].size() < ends[cu].size()) cu = c;
-      if ((int)ends[cu].size() >= slots) break;
-      const long long blk = pa::xcd_remap((int)g, (int)total);
-      ends[cu].push_back(done[cu] + (double)causal_block_tiles(nq - 1 - blk % nq, n, bm, bn));
-      g += pa::kNumXcd;
-    }
-    double dt = 0.0;
-    bool any = false;
-    for (size_t c = 0; c < ends.size(); ++c) {
-      if (ends[c].empty()) continue;
-      const double left = (*std::min_element(ends[c].begin(), ends[c].end()) - done[c]) * (double)ends[c].size();
-      if (!any || left < dt) dt = left;
-      any = true;
-    }
-    if (!any) break;
-    now += dt;
-    for (size_t c = 0; c < ends.size(); ++c) {
-      if (ends[c].empty()) continue;
-      done[c] += dt / (double)ends[c].size();
-      const double at = done[c] + 1e-9 * (1.0 + done[c]);
-      ends[c].erase(std::remove_if(ends[c].begin(), ends[c].end(), [&](double e) { return e <= at; }), ends[c].end());
-    }
-  }
-  return now;
-}
-
-struct CausalChoice {
-  bool persistent = false;
-  int by_rank = 0;
-};
-CausalChoice causal_choice(int64_t n, int64_t bh, int bm, int bn, int wgs, int slots, int cus, bool rank_only) {
-  if (wgs <= 0 || slots <= 0 || cus <= 0) return {};
-  const long long heads = (bh + pa::kNumXcd - 1) / pa::kNumXcd;
-  if (heads * ((n + bm - 1) / bm) > 64LL * cus) return {true, rank_only ? 1 : 0};
-  struct Entry {
-    int64_t n = -1, bh = -1;
-    int bm = 0, wgs = 0, slots = 0, cus = 0;
-    bool rank_only = false;
-    CausalChoice choice;
-  };
-  static std::mutex mu;
-  static Entry cache[64];
-  Entry& e = cache[(size_t)((uint64_t)(n * 1000003 + bh * 131 + bm + wgs) % 64)];
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    if (e.n == n && e.bh == bh && e.bm == bm && e.wgs == wgs && e.slots == slots && e.cus == cus &&
-        e.rank_only == rank_only)
-      return e.choice;
-  }
-  const long long by_rank = causal_walk_busiest(n, bh, bm, bn, wgs, cus, 1);
-  const long long by_head = rank_only ? by_rank + 1 : causal_walk_busiest(n, bh, bm, bn, wgs, cus, 0);
-  CausalChoice choice;
-  choice.by_rank = by_rank < by_head ? 1 : 0;
-  choice.persistent = per_block_makespan(n, bh, bm, bn, slots, cus) >= 0.85 * (double)std::min(by_rank, by_head);
-  std::lock_guard<std::mutex> lock(mu);
-  e.n = n; e.bh = bh; e.bm = bm; e.wgs = wgs; e.slots = slots; e.cus = cus; e.rank_only = rank_only;
-  e.choice = choice;
-  return choice;
-}
-
 // Grid of the persistent launch of this call, 0 for one workgroup per query block. A call that
 // needs the RAGGED form keeps the persistent launch only if that kernel fits as many workgroups
 // per CU as the clean one. It does at d = 128 (one workgroup per CU either way; padding an odd
@@ -285,7 +173,7 @@ PersistentPlan persistent_grid_for(int64_t n, int64_t bh, int causal) {
       return {};
     const int grid = persistent_grid(total, wpc);
     const int per_block = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false, false>();
-    const CausalChoice c = causal_choice(n, bh, BM, BN, grid / pa::kNumXcd, per_block, device_cus() / pa::kNumXcd, D == 64);
+    const pa::CausalChoice c = pa::causal_choice(n, bh, BM, BN, grid / pa::kNumXcd, per_block, device_cus() / pa::kNumXcd, D == 64);
     return c.persistent ? PersistentPlan{grid, c.by_rank} : PersistentPlan{};
   }
   const int clean = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, false>();

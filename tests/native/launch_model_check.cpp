@@ -1,0 +1,100 @@
+// Host-only checks of the causal walk and of the launch model (phantom-a100_amd/csrc/launch_model.hpp),
+// compiled and run by tests/test_launch_model.py on the CPU. Exit status 0 when every check holds;
+// each failure prints one line starting with FAIL.
+//
+// 1. The walk (causal_walk_block, the function the causal persistent kernel calls) hands every
+//    query block to exactly one workgroup, on the XCD that owns the block's head, for both list
+//    orders, both dealing branches (workgroups filling whole slots of the CUs, or not) and grids of
+//    one to three workgroups per CU, as the launcher sizes them.
+// 2. The model's figures for whole-head shapes against an independent restatement of the same model
+//    (per-CU tiles of each walk, and a processor-sharing simulation of the per-block launch), and
+//    the launch and walk it then chooses.
+#include <cstdio>
+#include <vector>
+
+#include "launch_model.hpp"
+
+static int failures = 0;
+#define CHECK(cond, ...)                    \
+  do {                                      \
+    if (!(cond)) {                          \
+      ++failures;                           \
+      std::printf("FAIL: " __VA_ARGS__);    \
+      std::printf("\n");                    \
+    }                                       \
+  } while (0)
+
+static void check_walk(int bh, int nq, int wpc, int cus, int by_rank) {
+  const long long total = (long long)bh * nq;
+  const int per_xcd = (int)((total + pa::kNumXcd - 1) / pa::kNumXcd);
+  const int wgs = std::min(std::max(cus, 32) * wpc, per_xcd);   // the launcher's grid per XCD
+  std::vector<int> seen((size_t)total, 0);
+  for (int x = 0; x < pa::kNumXcd; ++x)
+    for (int c = 0; c < wgs; ++c)
+      for (int j = 0;; ++j) {
+        const int blk = pa::causal_walk_block(j, c, x, wgs, cus, bh, nq, by_rank);
+        if (blk < 0) break;
+        if (blk >= total) {
+          CHECK(false, "bh=%d nq=%d wgs=%d cus=%d by_rank=%d: block %d out of range", bh, nq, wgs, cus, by_rank, blk);
+          break;
+        }
+        CHECK((blk / nq) % pa::kNumXcd == x, "bh=%d nq=%d by_rank=%d: block %d on XCD %d", bh, nq, by_rank, blk, x);
+        ++seen[(size_t)blk];
+      }
+  int missing = 0, repeated = 0;
+  for (int s : seen) {
+    missing += s == 0;
+    repeated += s > 1;
+  }
+  CHECK(missing == 0 && repeated == 0, "bh=%d nq=%d wgs=%d cus=%d by_rank=%d: %d blocks missing, %d repeated", bh, nq,
+        wgs, cus, by_rank, missing, repeated);
+}
+
+int main() {
+  int walks = 0;
+  for (int bh : {1, 2, 3, 5, 7, 8, 9, 12, 13, 16, 20, 42, 63, 64, 100, 128})
+    for (int nq : {1, 2, 3, 4, 5, 8, 9, 12, 16, 24, 63, 64})
+      for (int wpc : {1, 2, 3})
+        for (int cus : {32, 0})
+          for (int by_rank : {0, 1}) {
+            check_walk(bh, nq, wpc, cus, by_rank);
+            ++walks;
+          }
+  std::printf("walks checked: %d\n", walks);
+
+  struct Case {
+    int bh, n, d, slots;
+    long long by_head, by_rank;
+    double per_block;
+    int persistent, walk_by_rank;
+  };
+  // Figures of the independent restatement; the choice follows from them (0.85 rule, d = 64 by
+  // length, d = 128 by length only where its busiest CU is lower).
+  const Case cases[] = {
+      {128, 4096, 128, 1, 272, 272, 300.0, 1, 0},
+      {32, 3072, 128, 1, 84, 48, 60.0, 1, 1},
+      {128, 768, 128, 1, 24, 12, 20.0, 1, 1},
+      {128, 1030, 64, 3, 82, 46, 60.0, 1, 1},
+      {16, 8000, 64, 3, 376, 252, 312.0, 1, 1},
+      {64, 4096, 64, 3, 264, 264, 330.0, 1, 1},
+  };
+  for (const Case& k : cases) {
+    const int bm = k.d == 128 ? 256 : 128, bn = 64, cus = 32;
+    const long long total = (long long)(k.n + bm - 1) / bm * k.bh;
+    const int wgs = (int)std::min<long long>((long long)cus * k.slots, (total + 7) / 8);
+    const long long h = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 0);
+    const long long r = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 1);
+    const double p = pa::per_block_makespan(k.n, k.bh, bm, bn, k.slots, cus);
+    const pa::CausalChoice ch = pa::causal_choice(k.n, k.bh, bm, bn, wgs, k.slots, cus, k.d == 64);
+    std::printf("B*H=%d N=%d d=%d: busiest CU head by head %lld, by length %lld, per-block %.1f -> persistent %d, by length %d\n",
+                k.bh, k.n, k.d, h, r, p, (int)ch.persistent, ch.by_rank);
+    CHECK(h == k.by_head && r == k.by_rank, "B*H=%d N=%d d=%d: busiest %lld / %lld, expected %lld / %lld", k.bh, k.n,
+          k.d, h, r, k.by_head, k.by_rank);
+    CHECK(p > k.per_block - 1e-6 && p < k.per_block + 1e-6, "B*H=%d N=%d d=%d: per-block %.3f, expected %.3f", k.bh, k.n,
+          k.d, p, k.per_block);
+    CHECK((int)ch.persistent == k.persistent && ch.by_rank == k.walk_by_rank, "B*H=%d N=%d d=%d: choice %d/%d", k.bh,
+          k.n, k.d, (int)ch.persistent, ch.by_rank);
+  }
+  std::printf("%s\n", failures ? "FAILED" : "ok");
+  return failures ? 1 : 0;
+}

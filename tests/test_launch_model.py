@@ -1,0 +1,30 @@
+"""Host-only checks of the causal walk and the launch model (no GPU): builds and runs
+tests/native/launch_model_check.cpp with hipcc, which cross-compiles here without a device."""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+
+
+def hipcc():
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        pytest.skip("hipcc not found")
+    return path
+
+
+def test_causal_walk_and_launch_model(tmp_path):
+    exe = tmp_path / "launch_model_check"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "-I", os.path.join(REPO, "include"), "-I", os.path.join(REPO, "phantom-a100_amd", "csrc"),
+           os.path.join(HERE, "native", "launch_model_check.cpp"), "-o", str(exe)]
+    build = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert build.returncode == 0, build.stdout + build.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(run.stdout)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert run.stdout.strip().endswith("ok")
