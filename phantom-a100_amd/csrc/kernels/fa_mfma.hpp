@@ -81,11 +81,11 @@
 //    even count; its waves need the tiles up to min(N, their last row + 1). The c clean tiles run the clean persistent iterations; the diagonal tiles (with
 //    the two before them) run copies (DIAG) in which each wave takes the fast path up to its last
 //    tile and idles after it, the fast path masking S(t+1) when t+1 is the wave's diagonal tile;
-//    only the block's very last tile (the last wrap copy) takes the generic path. Blocks are
-//    dealt to the workgroups of an XCD in rounds of whole heads (longest block first within a
-//    head), in a serpentine order: the workgroup that gets a round's c-th longest block gets the
-//    next round's c-th shortest, so every workgroup gets the same number of tiles, while the
-//    blocks running at once on an XCD share the K/V of few heads in its L2.
+//    only the block's very last tile (the last wrap copy) takes the generic path. An XCD's blocks
+//    are listed head by head (longest first within a head; the blocks running at once then share
+//    the K/V of few heads in its L2) or by length across its heads (walk_by_rank), and dealt to
+//    its CUs in serpentine passes, so that a CU that gets one pass's long block gets the next
+//    pass's short one (causal_walk_block in common.hpp; the launcher picks the order).
 //  * The persistent forms stage each wave's block of O in LDS and store it as whole rows with
 //    non-temporal stores (store_block), so few dirty O lines are left for the end of the launch.
 #pragma once
