@@ -132,21 +132,25 @@ __host__ __device__ __forceinline__ int causal_walk_entry(int j, int c, int wgs,
 }
 
 // The causal walk: the query block (head * num_qblocks + block) that workgroup c of the wgs on
-// XCD x takes at step j, -1 past the end of the XCD's list. XCD x owns the heads x, x + 8, ...
-// below bh. Its list holds their blocks head by head, longest (last) block first within a head
-// (by_rank = 0), or by length, the longest block of every head first (by_rank = 1); the list is
-// dealt out by causal_walk_entry. Head by head, the blocks running at once on an XCD share the
-// K/V of few heads in its L2, and the serpentine passes pair long and short blocks on a CU
-// exactly when the blocks per head tile the passes; by length, the passes deal a sorted list,
-// which is near the longest-first greedy assignment for any block count.
-__host__ __device__ __forceinline__ int causal_walk_block(int j, int c, int x, int wgs, int cus_per_xcd, int bh,
-                                                          int num_qblocks, int by_rank) {
-  const int heads = (bh - x + kNumXcd - 1) / kNumXcd;
-  const int e = causal_walk_entry(j, c, wgs, cus_per_xcd);
+// list x takes at step j, -1 past the end of the list. The heads below bh are split over `lists`
+// lists, list x owning the heads x, x + lists, ...: one list per XCD (lists = kNumXcd, c and wgs
+// counted within the XCD, cus the XCD's CUs), or one for the device (lists = 1, c the workgroup
+// id, cus every CU: workgroup g runs on the device's CU g % cus, since the dispatcher sends g to
+// XCD g % 8 and places an XCD's workgroups on its CUs in turn). A list holds its blocks head by
+// head, longest (last) block first within a head (by_rank = 0), or by length, the longest block
+// of every head first (by_rank = 1), and is dealt out by causal_walk_entry. Head by head, the
+// blocks running at once on an XCD share the K/V of few heads in its L2, and the serpentine
+// passes pair long and short blocks on a CU exactly when the blocks per head tile the passes; by
+// length, the passes deal a sorted list, which is near the longest-first greedy assignment for any
+// block count.
+__host__ __device__ __forceinline__ int causal_walk_block(int j, int c, int x, int wgs, int cus, int bh,
+                                                          int num_qblocks, int by_rank, int lists) {
+  const int heads = (bh - x + lists - 1) / lists;
+  const int e = causal_walk_entry(j, c, wgs, cus);
   if (e >= heads * num_qblocks) return -1;
   const int h = by_rank ? e % heads : e / num_qblocks;
   const int r = by_rank ? e / heads : e % num_qblocks;
-  return (x + kNumXcd * h) * num_qblocks + (num_qblocks - 1 - r);
+  return (x + lists * h) * num_qblocks + (num_qblocks - 1 - r);
 }
 
 }  // namespace pa

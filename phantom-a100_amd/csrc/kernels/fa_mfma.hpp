@@ -83,9 +83,10 @@
 //    tile and idles after it, the fast path masking S(t+1) when t+1 is the wave's diagonal tile;
 //    only the block's very last tile (the last wrap copy) takes the generic path. An XCD's blocks
 //    are listed head by head (longest first within a head; the blocks running at once then share
-//    the K/V of few heads in its L2) or by length across its heads (walk_by_rank), and dealt to
-//    its CUs in serpentine passes, so that a CU that gets one pass's long block gets the next
-//    pass's short one (causal_walk_block in common.hpp; the launcher picks the order).
+//    the K/V of few heads in its L2) or by length across its heads, or the device's blocks by
+//    length in one list (for few heads), and dealt to the CUs in serpentine passes, so that a CU
+//    that gets one pass's long block gets the next pass's short one (causal_walk_block in
+//    common.hpp; the launcher picks the list).
 //  * The persistent forms stage each wave's block of O in LDS and store it as whole rows with
 //    non-temporal stores (store_block), so few dirty O lines are left for the end of the launch.
 #pragma once
@@ -144,7 +145,7 @@ __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT)
 __attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, RAGGED, CAUSAL>())))
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal,
-            int cus_per_xcd, int walk_by_rank) {
+            int cus_per_xcd, int walk) {
   typedef typename vec8<T>::type V8;
   typedef MfmaLds<D, BN, STAGES> L;
   constexpr float kLazyLog2 = 8.f;       // P stays below 2^kLazyLog2 between rescales
@@ -214,15 +215,18 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // Query block blk = (head, BM-query block). The persistent form walks the blocks of its XCD's
   // range (blk = x * range + c + C * j for the c-th of the C workgroups on XCD x), so that all
   // blocks of a head still run on one XCD.
-  // CAUSAL: XCD x owns the heads x, x + 8, x + 16, ... below B*H; its list holds their blocks
-  // head by head, or by length when walk_by_rank is set, and is dealt out in serpentine passes
-  // over the XCD's cus_per_xcd CUs (causal_walk_block), so the workgroups sharing a CU take blocks
-  // from opposite ends of the length order.
+  // CAUSAL: a list of query blocks per XCD, XCD x owning the heads x, x + 8, x + 16, ... below
+  // B*H, head by head (walk 0) or by length (walk 1); or one list for the device, by length
+  // (walk 2). A list is dealt out in serpentine passes over its CUs (causal_walk_block), so the
+  // workgroups sharing a CU take blocks from opposite ends of the length order.
   const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
-  int blk = 0, blk_step = 0, blk_end = 0, walk = 0;
+  int blk = 0, blk_step = 0, blk_end = 0, step = 0;
   auto causal_block = [&](int j) -> int {
+    if (walk == 2)
+      return causal_walk_block(j, (int)blockIdx.x, 0, (int)gridDim.x, cus_per_xcd * kNumXcd, total_blocks / num_qblocks,
+                               num_qblocks, 1, 1);
     return causal_walk_block(j, (int)blockIdx.x / kNumXcd, (int)blockIdx.x % kNumXcd, (int)gridDim.x / kNumXcd,
-                             cus_per_xcd, total_blocks / num_qblocks, num_qblocks, walk_by_rank);
+                             cus_per_xcd, total_blocks / num_qblocks, num_qblocks, walk, kNumXcd);
   };
   if constexpr (CAUSAL) {
     blk = causal_block(0);
@@ -794,7 +798,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       const std::integral_constant<int, 3> diag_wrap{};
       while (true) {
         if constexpr (CAUSAL) {
-          blk_n = causal_block(walk + 1);
+          blk_n = causal_block(step + 1);
           has_next = blk_n >= 0;
           // Tiles [0, c) are clean in every wave; the per-wave copies start two tiles before c.
           const int c = q0 / BN;
@@ -820,7 +824,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         }
         store_block();
         if (!has_next) break;
-        ++walk;
+        ++step;
         blk = blk_n;
         q0 = (blk % num_qblocks) * BM;
         q0w = q0 + wave * 32;
@@ -1008,7 +1012,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
       const std::integral_constant<int, 3> diag_wrap{};
       while (true) {
         if constexpr (CAUSAL) {
-          blk_n = causal_block(walk + 1);
+          blk_n = causal_block(step + 1);
           has_next = blk_n >= 0;
           // Tiles [0, c) are clean in every wave; the per-wave copies start two tiles before c.
           const int c = q0 / BN;
@@ -1034,7 +1038,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
         }
         store_block();
         if (!has_next) break;
-        ++walk;
+        ++step;
         blk = blk_n;
         q0 = (blk % num_qblocks) * BM;
         q0w = q0 + wave * 32;

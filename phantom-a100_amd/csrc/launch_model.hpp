@@ -42,12 +42,14 @@ inline long long causal_block_tiles(long long qb, int64_t n, int bm, int bn) {
   return t + (t & 1);   // padded to even, as the kernel pads it
 }
 
-inline long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus, int by_rank) {
+// Key tiles of the busiest CU under the walk of list 0 of `lists` (XCD 0 of the per-XCD lists,
+// the most heads; or the device's one list), wgs workgroups over cus CUs.
+inline long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus, int by_rank, int lists) {
   const int nq = (int)((n + bm - 1) / bm);
   std::vector<long long> load((size_t)cus, 0);
   for (int c = 0; c < wgs; ++c) {
     for (int j = 0;; ++j) {
-      const int blk = causal_walk_block(j, c, 0, wgs, cus, (int)bh, nq, by_rank);
+      const int blk = causal_walk_block(j, c, 0, wgs, cus, (int)bh, nq, by_rank, lists);
       if (blk < 0) break;
       load[(size_t)(c % cus)] += causal_block_tiles(blk % nq, n, bm, bn);
     }
@@ -55,12 +57,13 @@ inline long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int 
   return *std::max_element(load.begin(), load.end());
 }
 
-inline double per_block_makespan(int64_t n, int64_t bh, int bm, int bn, int slots, int cus) {
+// When the per-block launch's last block on XCD x ends (its cus CUs, `slots` blocks per CU).
+inline double per_block_makespan(int64_t n, int64_t bh, int bm, int bn, int slots, int cus, int x) {
   const long long nq = (n + bm - 1) / bm, total = nq * bh;
   std::vector<double> done((size_t)cus, 0.0);          // work each resident block of a CU has had
   std::vector<std::vector<double>> ends((size_t)cus);  // `done` at which each resident block ends
   double now = 0.0;
-  long long g = 0;   // next workgroup id of XCD 0
+  long long g = x;   // next workgroup id of XCD x
   while (true) {
     while (g < total) {
       size_t cu = 0;
@@ -91,18 +94,26 @@ inline double per_block_makespan(int64_t n, int64_t bh, int bm, int bn, int slot
   return now;
 }
 
+// The launch and walk for causal rows: walk 0 (per-XCD lists head by head), 1 (per-XCD lists by
+// length) or 2 (one list over the device by length). wgs: workgroups per XCD of the persistent
+// launch, slots: blocks per CU of the per-block launch, cus: CUs per XCD. per_xcd: whether the
+// per-XCD lists may be used (the launcher's heads rule); rank_only: no head-by-head lists. The
+// device list is taken over the per-XCD ones only where its busiest CU is 5 % lower (its blocks
+// of a head run on every XCD, so they share less K/V in L2).
 struct CausalChoice {
   bool persistent = false;
-  int by_rank = 0;
+  int walk = 0;
 };
-inline CausalChoice causal_choice(int64_t n, int64_t bh, int bm, int bn, int wgs, int slots, int cus, bool rank_only) {
+inline CausalChoice causal_choice(int64_t n, int64_t bh, int bm, int bn, int wgs, int slots, int cus, bool rank_only,
+                                  bool per_xcd) {
   if (wgs <= 0 || slots <= 0 || cus <= 0) return {};
-  const long long heads = (bh + kNumXcd - 1) / kNumXcd;
-  if (heads * ((n + bm - 1) / bm) > 64LL * cus) return {true, rank_only ? 1 : 0};
+  const long long nq = (n + bm - 1) / bm, heads = (bh + kNumXcd - 1) / kNumXcd;
+  if (per_xcd && heads * nq > 64LL * cus) return {true, rank_only ? 1 : 0};
+  if (!per_xcd && bh * nq > 64LL * cus * kNumXcd) return {true, 2};
   struct Entry {
     int64_t n = -1, bh = -1;
     int bm = 0, wgs = 0, slots = 0, cus = 0;
-    bool rank_only = false;
+    bool rank_only = false, per_xcd = false;
     CausalChoice choice;
   };
   static std::mutex mu;
@@ -111,16 +122,28 @@ inline CausalChoice causal_choice(int64_t n, int64_t bh, int bm, int bn, int wgs
   {
     std::lock_guard<std::mutex> lock(mu);
     if (e.n == n && e.bh == bh && e.bm == bm && e.wgs == wgs && e.slots == slots && e.cus == cus &&
-        e.rank_only == rank_only)
+        e.rank_only == rank_only && e.per_xcd == per_xcd)
       return e.choice;
   }
-  const long long by_rank = causal_walk_busiest(n, bh, bm, bn, wgs, cus, 1);
-  const long long by_head = rank_only ? by_rank + 1 : causal_walk_busiest(n, bh, bm, bn, wgs, cus, 0);
   CausalChoice choice;
-  choice.by_rank = by_rank < by_head ? 1 : 0;
-  choice.persistent = per_block_makespan(n, bh, bm, bn, slots, cus) >= 0.85 * (double)std::min(by_rank, by_head);
+  double best = 0.0;
+  if (per_xcd) {
+    const long long by_rank = causal_walk_busiest(n, bh, bm, bn, wgs, cus, 1, kNumXcd);
+    const long long by_head = rank_only ? by_rank + 1 : causal_walk_busiest(n, bh, bm, bn, wgs, cus, 0, kNumXcd);
+    choice.walk = by_rank < by_head ? 1 : 0;
+    best = (double)std::min(by_rank, by_head);
+  }
+  const double device = (double)causal_walk_busiest(n, bh, bm, bn, wgs * kNumXcd, cus * kNumXcd, 1, 1);
+  if (!per_xcd || device < 0.95 * best) {
+    choice.walk = 2;
+    best = device;
+  }
+  double per_block = 0.0;
+  for (int x = 0; x < kNumXcd; ++x) per_block = std::max(per_block, per_block_makespan(n, bh, bm, bn, slots, cus, x));
+  choice.persistent = per_block >= 0.85 * best;
   std::lock_guard<std::mutex> lock(mu);
   e.n = n; e.bh = bh; e.bm = bm; e.wgs = wgs; e.slots = slots; e.cus = cus; e.rank_only = rank_only;
+  e.per_xcd = per_xcd;
   e.choice = choice;
   return choice;
 }

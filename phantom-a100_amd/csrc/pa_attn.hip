@@ -105,25 +105,18 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
 // 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
 // C5 845 -> 890 (back to back), 605 -> 627 and 821 -> 859 under the flushing protocol.
-// Causal rows take the CAUSAL form when the XCDs, each owning whole heads, get about as many heads
-// each (below); N need not be a multiple of BM (a head's last block then ends past N, with rows
-// that are computed and not stored): its workgroups walk their XCD's heads round by round, so each gets the same number of key tiles (the per-block launch
-// leaves CUs idle between blocks of unequal length and ends with the most loaded CU).
+// Causal rows may take the CAUSAL form for any N (a head's last block then ends past N, with rows
+// that are computed and not stored) and any B*H; persistent_grid_for picks its walk and whether it
+// beats the per-block launch (which leaves CUs idle between blocks of unequal length and ends with
+// the most loaded CU).
 // (Only the two-stage fused_tc kernels without a key split have persistent forms; the caller,
 // persistent_grid_for, is instantiated for those alone.)
 bool persistent_launch(int64_t n, int bn, int64_t bh, int causal) {
+  (void)bh;
   if (!persistent_enabled()) return false;
   // (An odd count of full tiles is padded with an empty one; a single tile is not, since a bf16
   // row of one tile takes its P as two terms, which only the per-block launch does.)
-  // Causal: each XCD walks whole heads, so B*H not a multiple of 8 leaves some XCDs one head more;
-  // taken while that is at most 25 % above the mean (and, in persistent_grid_for, while every XCD
-  // has a block for each of its workgroups). Measured against the per-block launch, causal TFLOP/s:
-  // bf16 d = 128 N = 4096, B*H = 63 / 42 / 20: 961 -> 1182, 877 -> 931, 738 -> 886; B*H = 100,
-  // N = 1024: 485 -> 694; fp16 d = 64, B*H = 81, N = 2048: 558 -> 715. Outside the rule it lost:
-  // B*H = 12 (N = 4096, d = 128) 619 -> 601, fp16 d = 64 B*H = 42 N = 2048 (under one block per
-  // workgroup on every XCD, so a CU's three workgroups took blocks of one length) 453 -> 374.
-  const bool heads_even = (bh + pa::kNumXcd - 1) / pa::kNumXcd * pa::kNumXcd * 4 <= bh * 5;
-  return causal ? heads_even : ((n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn));
+  return causal || (n + bn - 1) / bn % 2 == 0 || (n % bn == 0 && n > bn);
 }
 // Workgroups of the persistent launch: wgs_per_cu per CU, at most as many per XCD as the XCD has
 // blocks.
@@ -159,7 +152,7 @@ int wgs_per_cu() {
 // 8x16x4050 908 -> 894, 1x16x8000 883 -> 920).
 struct PersistentPlan {
   int grid = 0;      // workgroups of the persistent launch, 0 for one workgroup per query block
-  int by_rank = 0;   // causal walk: blocks by length rather than head by head
+  int walk = 0;      // causal walk: 0 per-XCD lists head by head, 1 per-XCD lists by length, 2 one list
 };
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
 PersistentPlan persistent_grid_for(int64_t n, int64_t bh, int causal) {
@@ -168,13 +161,21 @@ PersistentPlan persistent_grid_for(int64_t n, int64_t bh, int causal) {
   const long long total = (n + BM - 1) / BM * bh;
   if (causal) {
     const int wpc = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, true>();
-    // B*H not a multiple of 8: every XCD needs at least one block per workgroup (its fewest heads).
-    if (bh % pa::kNumXcd != 0 && bh / pa::kNumXcd * ((n + BM - 1) / BM) < (long long)device_cus() / pa::kNumXcd * wpc)
-      return {};
+    const int cus = device_cus() / pa::kNumXcd;
+    // Per-XCD lists (each XCD owning whole heads) need B*H a multiple of 8, or else at most 25 %
+    // more heads on the busiest XCD than the mean and a block for every workgroup on every XCD
+    // (measured per XCD against the per-block launch, TFLOP/s: bf16 d = 128 N = 4096 B*H = 63 / 42
+    // / 20: 961 -> 1182, 877 -> 931, 738 -> 886; B*H = 100, N = 1024: 485 -> 694; fp16 d = 64,
+    // B*H = 81, N = 2048: 558 -> 715; outside the rule: B*H = 12 (N = 4096, d = 128) 619 -> 601,
+    // fp16 d = 64 B*H = 42 N = 2048, under a block per workgroup, 453 -> 374). Otherwise the walk
+    // takes one list over the device.
+    const bool per_xcd = bh % pa::kNumXcd == 0 ||
+                         ((bh + pa::kNumXcd - 1) / pa::kNumXcd * pa::kNumXcd * 4 <= bh * 5 &&
+                          bh / pa::kNumXcd * ((n + BM - 1) / BM) >= (long long)cus * wpc);
     const int grid = persistent_grid(total, wpc);
     const int per_block = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false, false>();
-    const pa::CausalChoice c = pa::causal_choice(n, bh, BM, BN, grid / pa::kNumXcd, per_block, device_cus() / pa::kNumXcd, D == 64);
-    return c.persistent ? PersistentPlan{grid, c.by_rank} : PersistentPlan{};
+    const pa::CausalChoice c = pa::causal_choice(n, bh, BM, BN, grid / pa::kNumXcd, per_block, cus, D == 64, per_xcd);
+    return c.persistent ? PersistentPlan{grid, c.walk} : PersistentPlan{};
   }
   const int clean = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, false>();
   if (n % (2 * BN) == 0) return {persistent_grid(total, clean), 0};
@@ -201,7 +202,7 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
         hipLaunchKernelGGL(kernel, dim3((unsigned)plan.grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                            static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal,
-                           device_cus() / pa::kNumXcd, plan.by_rank);
+                           device_cus() / pa::kNumXcd, plan.walk);
         return hipGetLastError();
       }
     }
@@ -545,7 +546,8 @@ const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, 
   snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s> grid %d x %d threads",
            dt_name[e->dtype], e->d, e->br, e->bc, e->db ? 2 : 1, dt_name[e->out_dtype],
            e->ks == 2 ? ", key split 2" : "", pers ? ", persistent" : "",
-           !pers ? "" : causal ? (plan.by_rank ? ", causal, by rank" : ", causal") : n % (2 * e->bc) ? ", ragged" : "",
+           !pers ? "" : !causal ? (n % (2 * e->bc) ? ", ragged" : "")
+                      : plan.walk == 2 ? ", causal, device list" : plan.walk == 1 ? ", causal, by rank" : ", causal",
            pers ? plan.grid : (int)total, e->br / 32 * pa::kWave * e->ks);
   return desc;
 }

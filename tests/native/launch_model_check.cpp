@@ -3,9 +3,10 @@
 // each failure prints one line starting with FAIL.
 //
 // 1. The walk (causal_walk_block, the function the causal persistent kernel calls) hands every
-//    query block to exactly one workgroup, on the XCD that owns the block's head, for both list
-//    orders, both dealing branches (workgroups filling whole slots of the CUs, or not) and grids of
-//    one to three workgroups per CU, as the launcher sizes them.
+//    query block to exactly one workgroup: with per-XCD lists on the XCD that owns the block's
+//    head, for both list orders, and with one list over the device; for both dealing branches
+//    (workgroups filling whole slots of the CUs, or not) and grids of one to three workgroups per
+//    CU, as the launcher sizes them.
 // 2. The model's figures for whole-head shapes against an independent restatement of the same model
 //    (per-CU tiles of each walk, and a processor-sharing simulation of the per-block launch), and
 //    the launch and walk it then chooses.
@@ -24,7 +25,8 @@ static int failures = 0;
     }                                       \
   } while (0)
 
-static void check_walk(int bh, int nq, int wpc, int cus, int by_rank) {
+// walk: 0 / 1 per-XCD lists head by head / by length, 2 one list over the device (by length).
+static void check_walk(int bh, int nq, int wpc, int cus, int walk) {
   const long long total = (long long)bh * nq;
   const int per_xcd = (int)((total + pa::kNumXcd - 1) / pa::kNumXcd);
   const int wgs = std::min(std::max(cus, 32) * wpc, per_xcd);   // the launcher's grid per XCD
@@ -32,13 +34,15 @@ static void check_walk(int bh, int nq, int wpc, int cus, int by_rank) {
   for (int x = 0; x < pa::kNumXcd; ++x)
     for (int c = 0; c < wgs; ++c)
       for (int j = 0;; ++j) {
-        const int blk = pa::causal_walk_block(j, c, x, wgs, cus, bh, nq, by_rank);
+        const int g = c * pa::kNumXcd + x;   // the workgroup id; the kernel's XCD is g % 8
+        const int blk = walk == 2 ? pa::causal_walk_block(j, g, 0, wgs * pa::kNumXcd, cus * pa::kNumXcd, bh, nq, 1, 1)
+                                  : pa::causal_walk_block(j, c, x, wgs, cus, bh, nq, walk, pa::kNumXcd);
         if (blk < 0) break;
         if (blk >= total) {
-          CHECK(false, "bh=%d nq=%d wgs=%d cus=%d by_rank=%d: block %d out of range", bh, nq, wgs, cus, by_rank, blk);
+          CHECK(false, "bh=%d nq=%d wgs=%d cus=%d walk=%d: block %d out of range", bh, nq, wgs, cus, walk, blk);
           break;
         }
-        CHECK((blk / nq) % pa::kNumXcd == x, "bh=%d nq=%d by_rank=%d: block %d on XCD %d", bh, nq, by_rank, blk, x);
+        CHECK(walk == 2 || (blk / nq) % pa::kNumXcd == x, "bh=%d nq=%d walk=%d: block %d on XCD %d", bh, nq, walk, blk, x);
         ++seen[(size_t)blk];
       }
   int missing = 0, repeated = 0;
@@ -46,8 +50,8 @@ static void check_walk(int bh, int nq, int wpc, int cus, int by_rank) {
     missing += s == 0;
     repeated += s > 1;
   }
-  CHECK(missing == 0 && repeated == 0, "bh=%d nq=%d wgs=%d cus=%d by_rank=%d: %d blocks missing, %d repeated", bh, nq,
-        wgs, cus, by_rank, missing, repeated);
+  CHECK(missing == 0 && repeated == 0, "bh=%d nq=%d wgs=%d cus=%d walk=%d: %d blocks missing, %d repeated", bh, nq,
+        wgs, cus, walk, missing, repeated);
 }
 
 int main() {
@@ -56,8 +60,8 @@ int main() {
     for (int nq : {1, 2, 3, 4, 5, 8, 9, 12, 16, 24, 63, 64})
       for (int wpc : {1, 2, 3})
         for (int cus : {32, 0})
-          for (int by_rank : {0, 1}) {
-            check_walk(bh, nq, wpc, cus, by_rank);
+          for (int walk : {0, 1, 2}) {
+            check_walk(bh, nq, wpc, cus, walk);
             ++walks;
           }
   std::printf("walks checked: %d\n", walks);
@@ -66,7 +70,7 @@ int main() {
     int bh, n, d, slots;
     long long by_head, by_rank;
     double per_block;
-    int persistent, walk_by_rank;
+    int persistent, walk;
   };
   // Figures of the independent restatement; the choice follows from them (0.85 rule, d = 64 by
   // length, d = 128 by length only where its busiest CU is lower).
@@ -82,18 +86,18 @@ int main() {
     const int bm = k.d == 128 ? 256 : 128, bn = 64, cus = 32;
     const long long total = (long long)(k.n + bm - 1) / bm * k.bh;
     const int wgs = (int)std::min<long long>((long long)cus * k.slots, (total + 7) / 8);
-    const long long h = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 0);
-    const long long r = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 1);
-    const double p = pa::per_block_makespan(k.n, k.bh, bm, bn, k.slots, cus);
-    const pa::CausalChoice ch = pa::causal_choice(k.n, k.bh, bm, bn, wgs, k.slots, cus, k.d == 64);
-    std::printf("B*H=%d N=%d d=%d: busiest CU head by head %lld, by length %lld, per-block %.1f -> persistent %d, by length %d\n",
-                k.bh, k.n, k.d, h, r, p, (int)ch.persistent, ch.by_rank);
+    const long long h = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 0, pa::kNumXcd);
+    const long long r = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 1, pa::kNumXcd);
+    const double p = pa::per_block_makespan(k.n, k.bh, bm, bn, k.slots, cus, 0);
+    const pa::CausalChoice ch = pa::causal_choice(k.n, k.bh, bm, bn, wgs, k.slots, cus, k.d == 64, true);
+    std::printf("B*H=%d N=%d d=%d: busiest CU head by head %lld, by length %lld, per-block %.1f -> persistent %d, walk %d\n",
+                k.bh, k.n, k.d, h, r, p, (int)ch.persistent, ch.walk);
     CHECK(h == k.by_head && r == k.by_rank, "B*H=%d N=%d d=%d: busiest %lld / %lld, expected %lld / %lld", k.bh, k.n,
           k.d, h, r, k.by_head, k.by_rank);
     CHECK(p > k.per_block - 1e-6 && p < k.per_block + 1e-6, "B*H=%d N=%d d=%d: per-block %.3f, expected %.3f", k.bh, k.n,
           k.d, p, k.per_block);
-    CHECK((int)ch.persistent == k.persistent && ch.by_rank == k.walk_by_rank, "B*H=%d N=%d d=%d: choice %d/%d", k.bh,
-          k.n, k.d, (int)ch.persistent, ch.by_rank);
+    CHECK((int)ch.persistent == k.persistent && ch.walk == k.walk, "B*H=%d N=%d d=%d: choice %d/%d", k.bh, k.n, k.d,
+          (int)ch.persistent, ch.walk);
   }
   std::printf("%s\n", failures ? "FAILED" : "ok");
   return failures ? 1 : 0;

@@ -523,25 +523,35 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     # d = 128 walks by length where head by head leaves some CU above the others
     ((2, 16, 3072), torch.bfloat16, 1.0, None, 128),
     ((4, 32, 1536), torch.float16, 3.0, torch.float32, 128),
+    # few heads: one list over the device
+    ((1, 4, 4096), torch.bfloat16, 1.0, None, 128),
+    ((1, 12, 1024), torch.bfloat16, 1.0, torch.float32, 128),
+    ((1, 1, 1000), torch.bfloat16, 3.0, None, 128),
+    ((1, 3, 2048), torch.float16, 3.0, torch.float32, 64),
+    ((2, 5, 3000), torch.float16, 1.0, None, 64),
+    ((1, 6, 4096), torch.bfloat16, 1.0, None, 64),
 ]
 
-# (B*H, N, d) -> the causal walk's order: head by head, or by length ("by rank").
+# (B*H, N, d) -> the causal walk: per-XCD lists head by head (""), per-XCD lists by length
+# (", by rank"), or one list over the device (", device list").
 CAUSAL_WALKS = [
-    ((128, 4096, 128), False),   # 16 blocks per head tile the passes
-    ((32, 8192, 128), False),
-    ((32, 3072, 128), True),     # 12 blocks per head do not
-    ((128, 1536, 128), True),
-    ((128, 1024, 64), True),     # d = 64 always by length
-    ((16, 8000, 64), True),
+    ((128, 4096, 128), ""),              # 16 blocks per head tile the passes
+    ((32, 8192, 128), ""),
+    ((32, 3072, 128), ", by rank"),      # 12 blocks per head do not
+    ((128, 1536, 128), ", by rank"),
+    ((128, 1024, 64), ", by rank"),      # d = 64 always by length
+    ((16, 8000, 64), ", by rank"),
+    ((4, 16384, 128), ", device list"),  # B*H below 8
+    ((12, 4096, 128), ", device list"),  # the busiest XCD 50 % above the mean
+    ((42, 2048, 64), ", device list"),   # fewer blocks than workgroups on some XCD
 ]
 
 
-@pytest.mark.parametrize("shape, by_rank", CAUSAL_WALKS)
-def test_causal_walk_order(shape, by_rank):
+@pytest.mark.parametrize("shape, walk", CAUSAL_WALKS)
+def test_causal_walk_order(shape, walk):
     bh, n, d = shape
     desc = _native.fused_tc_kernel(_native.DTYPE_BF16, _native.DTYPE_BF16, bh, n, d, True)
-    assert "persistent, causal" in desc, desc
-    assert ("by rank" in desc) == by_rank, desc
+    assert "persistent, causal" + walk + ">" in desc, desc
 
 
 @pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype, d", CAUSAL_PERSISTENT_SHAPES)
@@ -682,12 +692,12 @@ LONG_ROWS = [  # (N, d, dtype)
 
 
 @pytest.mark.parametrize("bh", [42, 12, 20])
-def test_causal_with_uneven_heads_per_xcd_takes_the_per_block_launch(bh):
+def test_causal_with_uneven_heads_per_xcd_takes_the_device_list(bh):
     """Causal B*H not a multiple of 8 whose whole heads per XCD would leave an XCD more than 25 %
     above the mean (12), or some XCD with fewer blocks than workgroups (42 and 20 at N = 1024,
-    d = 128), keeps the per-block launch, and still matches float64."""
+    d = 128), walks one list over the device, and still matches float64."""
     desc = _native.fused_tc_kernel(_native.DTYPE_BF16, _native.DTYPE_F32, bh, 1024, 128, True)
-    assert "persistent" not in desc, desc
+    assert "persistent, causal, device list" in desc, desc
     q, k, v = make_qkv(1, bh, 1024, 128, torch.bfloat16, seed=9, device="cuda")
     out = cuda_attn.fused_tc(q, k, v, True, out_dtype=torch.float32)
     heads = [0, bh - 1]
