@@ -12,12 +12,13 @@
 
 namespace pa {
 
-// Causal rows: which walk and which launch finish first, from a model of XCD 0 (it owns the most
-// heads), in key tiles at one CU's rate, the rate of a CU being shared by the workgroups it holds.
-// The persistent launch ends with its busiest CU: each CU's tiles summed over the blocks the walk
-// (causal_walk_block) deals its workgroups. The per-block launch is simulated: its blocks in
-// dispatch order (workgroup g to XCD g % 8, block xcd_remap(g)), each CU holding up to its
-// occupancy of them, a freed slot taking the next block on the CU that holds fewest.
+// Causal rows: which walk and which launch finish first, from a model in key tiles at one CU's
+// rate, the rate of a CU being shared by the workgroups it holds. The persistent launch ends with
+// its busiest CU (of XCD 0, which owns the most heads, for per-XCD lists): each CU's tiles summed
+// over the blocks the walk (causal_walk_block) deals its workgroups. The per-block launch is
+// simulated: its blocks in dispatch order (workgroup g to XCD g % 8, block xcd_remap(g)), each CU
+// holding up to its occupancy of them, a freed slot taking the next block on the CU that holds
+// fewest.
 // The walk's list runs head by head or by length. Head by head, the serpentine passes pair every
 // CU's long and short blocks only when the blocks per head tile the passes (4 to 64 blocks per head
 // at 32 CUs per XCD); other counts leave some CU 1.4-2.2x above the mean. By length, the passes
@@ -29,7 +30,12 @@ namespace pa {
 // 1x42x4096 938 -> 1015. At d = 64 (three workgroups per CU) by length was faster everywhere:
 // fp16 8x16x1024 644 -> 682, 1x16x8192 840 -> 890, 8x16x1030 461 -> 584, 1x16x8000 696 -> 884,
 // 4x16x1536 572 -> 732, 2x16x3072 602 -> 792, 1x16x6144 694 -> 823. So d = 64 walks by length, and
-// d = 128 by length only where the model's busiest CU is lower that way.
+// d = 128 by length only where the model's busiest CU is lower that way. Where per-XCD lists are
+// not allowed (few heads, or heads uneven over the XCDs) one list over the device, by length, is
+// modelled on all CUs; against the per-block launch it measured, TFLOP/s, bf16 d = 128 B*H x N =
+// 1x65536 661 -> 881, 4x16384 807 -> 862, 12x4096 607 -> 653, 42x1024 411 -> 433, fp16 d = 64
+// 4x16384 606 -> 681, 10x8192 500 -> 733, 42x2048 441 -> 651. The per-block launch is simulated on
+// every XCD, since with few heads `xcd_remap` gives one XCD the longest eighth of a head.
 // The persistent launch is then taken while the model's per-block time is at least 0.85 of the
 // persistent one: the measured per-block / persistent time ratio ran at the model's times 0.9-1.25
 // (the persistent launch also hides each block's start); e.g. head by head, model -> measured,
