@@ -222,11 +222,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   const uint32_t head_bytes = (uint32_t)((size_t)N * D * sizeof(T));
   int blk = 0, blk_step = 0, blk_end = 0, step = 0;
   auto causal_block = [&](int j) -> int {
-    if (walk == 2)
-      return causal_walk_block(j, (int)blockIdx.x, 0, (int)gridDim.x, cus_per_xcd * kNumXcd, total_blocks / num_qblocks,
-                               num_qblocks, 1, 1);
-    return causal_walk_block(j, (int)blockIdx.x / kNumXcd, (int)blockIdx.x % kNumXcd, (int)gridDim.x / kNumXcd,
-                             cus_per_xcd, total_blocks / num_qblocks, num_qblocks, walk, kNumXcd);
+    const int lists = walk == 2 ? 1 : kNumXcd;   // workgroup g is entry g / lists of list g % lists
+    return causal_walk_block(j, (int)blockIdx.x / lists, (int)blockIdx.x % lists, (int)gridDim.x / lists,
+                             cus_per_xcd * (kNumXcd / lists), total_blocks / num_qblocks, num_qblocks, walk != 0, lists);
   };
   if constexpr (CAUSAL) {
     blk = causal_block(0);
