@@ -20,22 +20,24 @@ pytestmark = pytest.mark.gpu
 
 # (entry, shape, dtype, causal, kwargs); the first GRAPH_CASES also run under graph capture (the
 # unfused entries allocate their score workspace per call). The causal fused_tc cases take the
-# causal persistent launch (B*H a multiple of 8).
+# causal persistent launch: per-XCD lists (B*H a multiple of 8), and one list over the device
+# (B*H = 4).
 CASES = [
     ("fused_tc", (2, 8, 512, 128), torch.bfloat16, False, {}),
     ("fused_tc", (2, 8, 1000, 64), torch.float16, False, {}),
     ("fused_tc", (2, 8, 1024, 128), torch.bfloat16, True, {}),
     ("fused_tc", (2, 8, 512, 64), torch.float16, True, {}),
+    ("fused_tc", (1, 4, 2048, 128), torch.bfloat16, True, {}),
     ("fused_tuned", (1, 8, 512, 64), torch.float16, False, {"br": 128, "bc": 64, "double_buffer": True}),
     ("fused", (1, 8, 256, 64), torch.float32, False, {}),
     ("tiled", (1, 4, 256, 64), torch.float32, False, {}),
     ("tiled", (1, 4, 512, 64), torch.float16, True, {}),
 ]
-GRAPH_CASES = 6
+GRAPH_CASES = 7
 
 
 def case_id(c):
-    return f"{c[0]}-{str(c[2])[6:]}" + ("-causal" if c[3] else "")
+    return f"{c[0]}-{str(c[2])[6:]}-{c[1][1] * c[1][0]}x{c[1][2]}x{c[1][3]}" + ("-causal" if c[3] else "")
 
 
 @pytest.mark.parametrize("name, shape, dtype, causal, kw", CASES, ids=[case_id(c) for c in CASES])
