@@ -20,8 +20,8 @@
  *     PA_ERR_* code for a rejected argument. pa_last_error() then returns a message for the
  *     calling thread (the reference turned cudaError_t into RuntimeError through ATTN_CHECK,
  *     csrc/common.cuh:21-25).
- *   - Every entry point is re-entrant; the only state is a thread-local error string and a
- *     per-device attribute cache.
+ *   - Every entry point is re-entrant; the only state is a thread-local error string, a
+ *     per-device attribute cache and a per-shape cache of the causal launch choice.
  */
 #ifndef PHANTOM_ATTN_H_
 #define PHANTOM_ATTN_H_
