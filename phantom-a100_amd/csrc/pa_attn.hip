@@ -111,8 +111,7 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // the most loaded CU).
 // (Only the two-stage fused_tc kernels without a key split have persistent forms; the caller,
 // persistent_grid_for, is instantiated for those alone.)
-bool persistent_launch(int64_t n, int bn, int64_t bh, int causal) {
-  (void)bh;
+bool persistent_launch(int64_t n, int bn, int causal) {
   if (!persistent_enabled()) return false;
   // (An odd count of full tiles is padded with an empty one; a single tile is not, since a bf16
   // row of one tile takes its P as two terms, which only the per-block launch does.)
@@ -157,7 +156,7 @@ struct PersistentPlan {
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS>
 PersistentPlan persistent_grid_for(int64_t n, int64_t bh, int causal) {
   static_assert(ST == 2 && KS == 1, "persistent forms: two stages, no key split");
-  if (!persistent_launch(n, BN, bh, causal)) return {};
+  if (!persistent_launch(n, BN, causal)) return {};
   const long long total = (n + BM - 1) / BM * bh;
   if (causal) {
     const int wpc = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, true>();
