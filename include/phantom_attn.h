@@ -20,8 +20,8 @@
  *     PA_ERR_* code for a rejected argument. pa_last_error() then returns a message for the
  *     calling thread (the reference turned cudaError_t into RuntimeError through ATTN_CHECK,
  *     csrc/common.cuh:21-25).
- *   - Every entry point is re-entrant; the only state is a thread-local error string, a
- *     per-device attribute cache and a per-shape cache of the causal launch choice.
+ *   - Every entry point is re-entrant; the only state is a thread-local error string and a
+ *     per-device attribute cache.
  */
 #ifndef PHANTOM_ATTN_H_
 #define PHANTOM_ATTN_H_
@@ -87,10 +87,9 @@ int pa_fused_tuned_fwd(const void* q, const void* k, const void* v, void* o,
  * dtype: F16 or BF16; out_dtype: dtype or F32; d in {64, 128}.
  * The launch is persistent (as many workgroups as fit on the device at once, walking the query
  * blocks) for causal == 0 with an even number of 64-key tiles (or an odd number, above one, of
- * full ones), and for causal != 0 where a model of both launches (the walk's tiles per CU
- * against the hardware's dispatch of one workgroup per query block) does not find the per-block
- * launch faster; unless pa_set_persistent(0) switched that off (see below). Otherwise one
- * workgroup per query block. pa_fused_tc_kernel names the choice.
+ * full ones), and for every causal != 0 call (its walk over the query blocks chosen from the
+ * shape); unless pa_set_persistent(0) switched that off (see below). Otherwise one workgroup per
+ * query block. pa_fused_tc_kernel names the choice.
  * Both launches give the same bits.
  * Replaces attn::launch_fused_tc (csrc/kernels/fused_tc.cuh:187-196) and fused_tc_forward
  * (csrc/attn_fused_tc.cu:5-19). */

@@ -110,8 +110,7 @@ __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 // same XCD: the dispatcher sends workgroup g to XCD g % 8, so logical id
 // (g % 8) * (total / 8) + g / 8 keeps a contiguous range of (head, query-block) pairs - the
 // blocks that re-read the same K/V rows - inside one XCD's L2. Identity when total % 8 != 0.
-// (The launcher's model of the per-block launch evaluates it on the host.)
-__host__ __device__ __forceinline__ int xcd_remap(int g, int total) {
+__device__ __forceinline__ int xcd_remap(int g, int total) {
   if (total % kNumXcd != 0) return g;
   return (g % kNumXcd) * (total / kNumXcd) + g / kNumXcd;
 }

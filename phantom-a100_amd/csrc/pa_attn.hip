@@ -105,10 +105,10 @@ bool persistent_enabled() { return g_persistent.load(std::memory_order_relaxed) 
 // d = 128: bf16 1125 / 1198 / 1062 / 929 -> 1184 / 1247 / 1126 / 1049, fp16 1021 / 1081 / 967 /
 // 868 -> 1043 / 1099 / 1002 / 941; at d = 64 fp16 (three workgroups per CU): C3 681 -> 708,
 // C5 845 -> 890 (back to back), 605 -> 627 and 821 -> 859 under the flushing protocol.
-// Causal rows may take the CAUSAL form for any N (a head's last block then ends past N, with rows
-// that are computed and not stored) and any B*H; persistent_grid_for picks its walk and whether it
-// beats the per-block launch (which leaves CUs idle between blocks of unequal length and ends with
-// the most loaded CU).
+// Causal rows take the CAUSAL form for any N (a head's last block then ends past N, with rows that
+// are computed and not stored) and any B*H, with the walk persistent_grid_for picks: faster than
+// one workgroup per block (which leaves CUs idle between blocks of unequal length and ends with the
+// most loaded CU) in every causal shape measured (launch_model.hpp).
 // (Only the two-stage fused_tc kernels without a key split have persistent forms; the caller,
 // persistent_grid_for, is instantiated for those alone.)
 bool persistent_launch(int64_t n, int bn, int causal) {
@@ -172,9 +172,8 @@ PersistentPlan persistent_grid_for(int64_t n, int64_t bh, int causal) {
                          ((bh + pa::kNumXcd - 1) / pa::kNumXcd * pa::kNumXcd * 4 <= bh * 5 &&
                           bh / pa::kNumXcd * ((n + BM - 1) / BM) >= (long long)cus * wpc);
     const int grid = persistent_grid(total, wpc);
-    const int per_block = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, false, false, false>();
-    const pa::CausalChoice c = pa::causal_choice(n, bh, BM, BN, grid / pa::kNumXcd, per_block, cus, D == 64, per_xcd);
-    return c.persistent ? PersistentPlan{grid, c.walk} : PersistentPlan{};
+    if (grid <= 0) return {};
+    return {grid, pa::causal_walk(n, bh, BM, BN, grid / pa::kNumXcd, cus, D == 64, per_xcd)};
   }
   const int clean = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, false>();
   if (n % (2 * BN) == 0) return {persistent_grid(total, clean), 0};

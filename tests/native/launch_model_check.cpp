@@ -7,9 +7,8 @@
 //    head, for both list orders, and with one list over the device; for both dealing branches
 //    (workgroups filling whole slots of the CUs, or not) and grids of one to three workgroups per
 //    CU, as the launcher sizes them.
-// 2. The model's figures for whole-head shapes against an independent restatement of the same model
-//    (per-CU tiles of each walk, and a processor-sharing simulation of the per-block launch), and
-//    the launch and walk it then chooses.
+// 2. The busiest CU's key tiles under each per-XCD walk, for whole-head shapes, against an
+//    independent restatement, and the walk the launcher then takes.
 #include <cstdio>
 #include <vector>
 
@@ -69,18 +68,17 @@ int main() {
   struct Case {
     int bh, n, d, slots;
     long long by_head, by_rank;
-    double per_block;
-    int persistent, walk;
+    int walk;
   };
-  // Figures of the independent restatement; the choice follows from them (0.85 rule, d = 64 by
-  // length, d = 128 by length only where its busiest CU is lower).
+  // Figures of the independent restatement; the walk follows from them (d = 64 by length, d = 128
+  // by length only where its busiest CU is lower).
   const Case cases[] = {
-      {128, 4096, 128, 1, 272, 272, 300.0, 1, 0},
-      {32, 3072, 128, 1, 84, 48, 60.0, 1, 1},
-      {128, 768, 128, 1, 24, 12, 20.0, 1, 1},
-      {128, 1030, 64, 3, 82, 46, 60.0, 1, 1},
-      {16, 8000, 64, 3, 376, 252, 312.0, 1, 1},
-      {64, 4096, 64, 3, 264, 264, 330.0, 1, 1},
+      {128, 4096, 128, 1, 272, 272, 0},
+      {32, 3072, 128, 1, 84, 48, 1},
+      {128, 768, 128, 1, 24, 12, 1},
+      {128, 1030, 64, 3, 82, 46, 1},
+      {16, 8000, 64, 3, 376, 252, 1},
+      {64, 4096, 64, 3, 264, 264, 1},
   };
   for (const Case& k : cases) {
     const int bm = k.d == 128 ? 256 : 128, bn = 64, cus = 32;
@@ -88,17 +86,14 @@ int main() {
     const int wgs = (int)std::min<long long>((long long)cus * k.slots, (total + 7) / 8);
     const long long h = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 0, pa::kNumXcd);
     const long long r = pa::causal_walk_busiest(k.n, k.bh, bm, bn, wgs, cus, 1, pa::kNumXcd);
-    const double p = pa::per_block_makespan(k.n, k.bh, bm, bn, k.slots, cus, 0);
-    const pa::CausalChoice ch = pa::causal_choice(k.n, k.bh, bm, bn, wgs, k.slots, cus, k.d == 64, true);
-    std::printf("B*H=%d N=%d d=%d: busiest CU head by head %lld, by length %lld, per-block %.1f -> persistent %d, walk %d\n",
-                k.bh, k.n, k.d, h, r, p, (int)ch.persistent, ch.walk);
+    const int walk = pa::causal_walk(k.n, k.bh, bm, bn, wgs, cus, k.d == 64, true);
+    std::printf("B*H=%d N=%d d=%d: busiest CU head by head %lld, by length %lld -> walk %d\n", k.bh, k.n, k.d, h, r, walk);
     CHECK(h == k.by_head && r == k.by_rank, "B*H=%d N=%d d=%d: busiest %lld / %lld, expected %lld / %lld", k.bh, k.n,
           k.d, h, r, k.by_head, k.by_rank);
-    CHECK(p > k.per_block - 1e-6 && p < k.per_block + 1e-6, "B*H=%d N=%d d=%d: per-block %.3f, expected %.3f", k.bh, k.n,
-          k.d, p, k.per_block);
-    CHECK((int)ch.persistent == k.persistent && ch.walk == k.walk, "B*H=%d N=%d d=%d: choice %d/%d", k.bh, k.n, k.d,
-          (int)ch.persistent, ch.walk);
+    CHECK(walk == k.walk, "B*H=%d N=%d d=%d: walk %d, expected %d", k.bh, k.n, k.d, walk, k.walk);
   }
+  // Heads the per-XCD lists may not take walk one list over the device.
+  CHECK(pa::causal_walk(16384, 4, 256, 64, 8, 32, false, false) == 2, "B*H=4: walk not the device list");
   std::printf("%s\n", failures ? "FAILED" : "ok");
   return failures ? 1 : 0;
 }
