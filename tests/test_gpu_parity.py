@@ -554,6 +554,39 @@ def test_causal_walk_order(shape, walk):
     assert "persistent, causal" + walk + ">" in desc, desc
 
 
+def random_causal_shapes(count=24, seed=2024):
+    """Seeded causal shapes over every walk: B*H 1-200 (a third of them 1-12, the device list), N
+    1-5000 (work bounded), d 64 / 128."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        bh = int(rng.integers(1, 13)) if rng.random() < 0.35 else int(rng.integers(1, 201))
+        n = int(rng.integers(1, 5001))
+        d = int(rng.choice([64, 128]))
+        if bh * n * n * d > 2.0e11:   # about 1 ms of work or less each
+            continue
+        out.append((bh, n, d, bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("bh, n, d, bf16", random_causal_shapes())
+def test_causal_walks_match_per_block_on_random_shapes(bh, n, d, bf16, per_block_launch):
+    """Whatever walk the launcher picks for a shape, the causal persistent form gives the per-block
+    launch's bits (the walk hands every query block to exactly one workgroup)."""
+    dtype = torch.bfloat16 if bf16 else torch.float16
+    code = _native.DTYPE_BF16 if bf16 else _native.DTYPE_F16
+    per_block_launch(True)
+    desc = _native.fused_tc_kernel(code, code, bh, n, d, True)
+    print(f"[random causal] bh={bh} n={n} d={d} {dtype}: {desc}", flush=True)
+    q, k, v = make_qkv(1, bh, n, d, dtype, seed=bh * 7919 + n, device="cuda")
+    got = cuda_attn.fused_tc(q, k, v, True)
+    per_block_launch(False)
+    want = cuda_attn.fused_tc(q, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.isfinite(got).all()
+
+
 @pytest.mark.parametrize("shape, dtype, qk_scale, out_dtype, d", CAUSAL_PERSISTENT_SHAPES)
 def test_causal_persistent_form_matches_per_block_form(shape, dtype, qk_scale, out_dtype, d, per_block_launch):
     b, h, n = shape
