@@ -530,6 +530,11 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((1, 3, 2048), torch.float16, 3.0, torch.float32, 64),
     ((2, 5, 3000), torch.float16, 1.0, None, 64),
     ((1, 6, 4096), torch.bfloat16, 1.0, None, 64),
+    # extremes: one query, many heads of one short tile, a row one past a tile
+    ((1, 1, 1), torch.bfloat16, 1.0, torch.float32, 128),
+    ((64, 64, 16), torch.float16, 3.0, None, 64),
+    ((2, 3, 65), torch.float16, 1.0, torch.float32, 128),
+    ((1, 3, 129), torch.bfloat16, 10.0, None, 128),
 ]
 
 # (B*H, N, d) -> the causal walk: per-XCD lists head by head (""), per-XCD lists by length
