@@ -71,6 +71,43 @@ __device__ __forceinline__ float partner32(float x) {
 __device__ __forceinline__ float half_max(float x) { return fmaxf(x, partner32(x)); }
 __device__ __forceinline__ float half_sum(float x) { return x + partner32(x); }
 
+// x[l ^ 16], on v_permlane16_swap: with vdst = vsrc = x it leaves vdst = x of the even 16-lane row
+// of each pair and vsrc = x of the odd one, so the partner is vsrc in even rows and vdst in odd
+// ones (the same selection by lane bit as partner32).
+__device__ __forceinline__ float partner16(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+
+// x of another lane of the same 16-lane row through a DPP move (CTRL: quad_perm 0x00-0xff,
+// row_mirror 0x140, row_half_mirror 0x141).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Wave64 all-reduce without LDS or ds_bpermute: every lane ends with op over all 64 lanes. Within
+// a 16-lane row, two quad permutations (lane ^ 1, lane ^ 2) make every quad uniform, the half-row
+// mirror (lane 7 - i within 8) pairs the two quads of an 8-lane half and the row mirror (lane
+// 15 - i) the two halves; then the 16- and 32-lane partner swaps join the four rows. op must be
+// commutative and associative (max, or + up to the order of its roundings, fixed per lane).
+template <typename Op>
+__device__ __forceinline__ float wave_allreduce(float x, Op op) {
+  x = op(x, dpp_move<0xB1>(x));    // quad_perm [1, 0, 3, 2]
+  x = op(x, dpp_move<0x4E>(x));    // quad_perm [2, 3, 0, 1]
+  x = op(x, dpp_move<0x141>(x));   // row_half_mirror
+  x = op(x, dpp_move<0x140>(x));   // row_mirror
+  x = op(x, partner16(x));
+  return op(x, partner32(x));
+}
+struct MaxOp {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct SumOp {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+
 // Buffer resource over [base, base + bytes): raw buffer loads at offsets past `bytes` return 0
 // without touching memory, which makes the tails of K/V/Q tiles branch-free.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;

@@ -9,9 +9,10 @@
 //         for fp16 inputs (scores at d a multiple of 16, P.V at d = 64 / 128) and for fp32 inputs
 //         at d = 64 / 128 (tiled_*_mfma, tiled_*_mfma_f32); otherwise 64x64 output tiles with 4x4
 //         register blocking per thread and LDS-staged operands. Softmax with one wave per row,
-//         the row held in registers up to 8192 keys (one read of S), else an online max/sum per
-//         lane and a 6-step butterfly merge across the 64 lanes. Causal P.V skips key tiles right
-//         of the diagonal.
+//         the row held in registers up to 8192 keys (one read of S); longer rows take one
+//         workgroup per row, in register-held segments whose max the workgroup agrees on before
+//         their sums (one read of S up to 32768 keys, two beyond). Causal P.V skips key tiles
+//         right of the diagonal.
 #pragma once
 
 #include "common.hpp"
@@ -46,7 +47,7 @@ naive_scores(const T* __restrict__ Q, const T* __restrict__ K, float* __restrict
 }
 
 // Row r of S in place: max, sum of exp(s - max), then exp(s - max) / sum, each a strided pass
-// of the wave's 64 lanes over the row followed by a butterfly reduction across the lanes.
+// of the wave's 64 lanes over the row followed by a wave all-reduce (DPP and lane swaps).
 __global__ void __launch_bounds__(256)
 naive_softmax(float* __restrict__ S, int N, long long rows) {
   const long long r = (long long)blockIdx.x * 4 + threadIdx.x / kWave;
@@ -55,10 +56,10 @@ naive_softmax(float* __restrict__ S, int N, long long rows) {
   float* srow = S + r * N;
   float mx = -INFINITY;
   for (int j = lane; j < N; j += kWave) mx = fmaxf(mx, srow[j]);
-  for (int w = kWave / 2; w >= 1; w /= 2) mx = fmaxf(mx, __shfl_xor(mx, w));
+  mx = wave_allreduce(mx, MaxOp{});
   float sum = 0.f;
   for (int j = lane; j < N; j += kWave) sum += expf(srow[j] - mx);
-  for (int w = kWave / 2; w >= 1; w /= 2) sum += __shfl_xor(sum, w);
+  sum = wave_allreduce(sum, SumOp{});
   const float rcp = 1.f / sum;
   for (int j = lane; j < N; j += kWave) srow[j] = expf(srow[j] - mx) * rcp;
 }
@@ -133,14 +134,6 @@ tiled_scores(const T* __restrict__ Q, const T* __restrict__ K, float* __restrict
       if (j < N) S[((size_t)bh * N + i) * N + j] = (causal && j > i) ? -INFINITY : acc[u][w] * scale;
     }
   }
-}
-
-// Merge partial softmax states (m, l) with l = sum exp(x - m); empty states have m = -inf.
-__device__ __forceinline__ void merge_state(float& m, float& l, float m2, float l2) {
-  const float mn = fmaxf(m, m2);
-  if (mn == -INFINITY) return;
-  l = l * expf(m - mn) + l2 * expf(m2 - mn);
-  m = mn;
 }
 
 // S = scale * Q K^T on the matrix core, for fp16 storage and d = 16 * KSTEPS (the tiled_scores
@@ -258,7 +251,7 @@ tiled_scores_mfma_f32(const float* __restrict__ Q, const float* __restrict__ K, 
 }
 
 // One wave per row, the whole row held in registers (rows of at most 64 * VPL keys): S is read
-// once and P written once, 8 bytes per score (the two-pass kernel below reads S twice). The max
+// once and P written once, 8 bytes per score (the naive softmax reads S three times). The max
 // first, then the sum of exp(x - max) kept in place, then P = e / sum; element j of the row sits in
 // lane j % 64, slot j / 64, so every load and store of a wave covers 256 contiguous bytes.
 template <int VPL>
@@ -277,16 +270,14 @@ tiled_softmax_rows(float* __restrict__ S, int N) {
     x[k] = j < N ? row[j] : -INFINITY;
     m = fmaxf(m, x[k]);
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  m = wave_allreduce(m, MaxOp{});
   float l = 0.f;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     x[k] = expf(x[k] - m);   // -inf (masked or past N) -> 0; every row has a finite score
     l += x[k];
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+  l = wave_allreduce(l, SumOp{});
   const float inv = 1.f / l;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
@@ -295,41 +286,79 @@ tiled_softmax_rows(float* __restrict__ S, int N) {
   }
 }
 
-// One wave per row, 4 rows per 256-thread workgroup (rows longer than the register-held ones).
+// Rows longer than the one-wave register kernel holds (N > 64 * 128): one 256-lane workgroup per
+// row. The row is cut into segments of 256 * VPL keys, each held in registers (key
+// j0 + 256 k + t in slot k of thread t, so every load and store of a wave covers 256 contiguous
+// bytes). Per segment, the workgroup first agrees on the segment's max (wave all-reduce, then the
+// four wave maxima through LDS); where it exceeds the row's running max m, the per-thread sums are
+// multiplied by exp(m - m_new) once, and then every key of the segment adds exp(x - m) against the
+// same, workgroup-uniform m. So m needs no per-lane state and the end is a plain sum. A row of one
+// segment (N <= 256 * VPL) keeps its exponentials in registers and writes P from them (S read
+// once); longer rows read each segment again for P = exp(x - m) / l.
+template <int VPL>
 __global__ void __launch_bounds__(256)
-tiled_softmax(float* __restrict__ S, int N) {
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int bh = blockIdx.y;
-  const int i = blockIdx.x * 4 + wave;
-  if (i >= N) return;  // whole wave leaves together
-  float* row = S + ((size_t)bh * N + i) * N;
+tiled_softmax_segments(float* __restrict__ S, int N) {
+  constexpr int SEG = 256 * VPL;
+  // Two slots so that consecutive reductions need one barrier each: reduction r writes slot r % 2
+  // after every thread has passed reduction r - 1's barrier, i.e. after the reads of slot r % 2 by
+  // reduction r - 2.
+  __shared__ float part[2][4];
+  const int t = (int)threadIdx.x, wave = t / kWave, lane = t % kWave;
+  float* row = S + ((size_t)blockIdx.y * N + blockIdx.x) * N;
+  int slot = 0;
+  auto block_reduce = [&](float v, auto op) {
+    v = wave_allreduce(v, op);
+    if (lane == 0) part[slot][wave] = v;
+    __syncthreads();
+    const float r = op(op(part[slot][0], part[slot][1]), op(part[slot][2], part[slot][3]));
+    slot ^= 1;
+    return r;
+  };
+  const int segments = (N + SEG - 1) / SEG;
+  float x[VPL];
   float m = -INFINITY, l = 0.f;
-  for (int j = lane; j < N; j += kWave) {
-    const float x = row[j];
-    if (x > m) {
-      l = l * expf(m - x) + 1.f;
-      m = x;
-    } else if (x != -INFINITY) {
-      l += expf(x - m);
+  for (int sg = 0; sg < segments; ++sg) {
+    const int j0 = sg * SEG;
+    float smax = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int j = j0 + k * 256 + t;
+      x[k] = j < N ? row[j] : -INFINITY;
+      smax = fmaxf(smax, x[k]);
+    }
+    smax = block_reduce(smax, MaxOp{});
+    if (smax > m) {   // workgroup-uniform; l is still 0 while m is -inf
+      l = m == -INFINITY ? 0.f : l * expf(m - smax);
+      m = smax;
+    }
+    // Key 0 is visible in every row (causal or not), so m is finite from the first segment on.
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      x[k] = expf(x[k] - m);   // masked or past N: exp(-inf) = 0
+      l += x[k];
     }
   }
+  const float inv = 1.f / block_reduce(l, SumOp{});
+  if (segments == 1) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float m2 = __shfl_xor(m, off);
-    const float l2 = __shfl_xor(l, off);
-    merge_state(m, l, m2, l2);
+    for (int k = 0; k < VPL; ++k) {
+      const int j = k * 256 + t;
+      if (j < N) row[j] = x[k] * inv;
+    }
+  } else {
+    for (int j = t; j < N; j += 256) row[j] = expf(row[j] - m) * inv;
   }
-  const float inv = 1.f / l;
-  for (int j = lane; j < N; j += kWave) row[j] = expf(row[j] - m) * inv;
 }
 
 // O = P V on the matrix core for fp16 V with D in {64, 128} (the fused kernel's V operand path),
 // computed transposed as O^T += V^T P^T per 16-key step with v_mfma_f32_32x32x16_f16: A = V^T,
 // read from a swizzled LDS tile of 64 keys with ds_read_b64_tr_b16; B = P^T, lane l taking the 8
 // probabilities of its query row l % 32 at the keys the V reads pair with them (two runs of 4
-// consecutive keys) straight from the fp32 workspace. P is fed as two fp16 terms of 1024 P (hi = round(1024 P), lo = round(1024 P - hi),
-// ~22 significant bits, the lo term clear of fp16's subnormals for P >= 2^-24), both products exact
-// in fp32 and summed in fp32; O is scaled back by 2^-10. 128 queries per workgroup (32 per wave),
+// consecutive keys) straight from the fp32 workspace. P is fed as two fp16 terms of 1024 P
+// (hi = round(1024 P), lo = round(1024 P - hi)): ~22 significant bits while lo is a normal fp16
+// (|lo| ~ 2^-11 |hi| >= 2^-14, i.e. P >= ~2^-13); below that lo lands on fp16's subnormal spacing
+// 2^-24, so the pair is off by at most 2^-25 in 1024 P, 2^-35 in P. Both products are exact in
+// fp32 and summed in fp32; O is scaled back by 2^-10. 128 queries per workgroup (32 per wave),
 // two V stages; the next tile's V (to LDS) and P (to registers) load during the current one.
 // Reads past the head (query or key rows past N) return zero through the buffers' ranges, and
 // keys past N meet zero V rows. With causal, keys after the block's last query are skipped (their

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 #include <vector>
 
 #include "kernels/common.hpp"
@@ -60,6 +61,30 @@ inline long long causal_walk_busiest(int64_t n, int64_t bh, int bm, int bn, int 
   return *std::max_element(load.begin(), load.end());
 }
 
+// Per-XCD lists by length (1) or head by head (0), whichever leaves XCD 0's busiest CU fewer tiles.
+inline int causal_walk_uncached(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus) {
+  return causal_walk_busiest(n, bh, bm, bn, wgs, cus, 1, kNumXcd) < causal_walk_busiest(n, bh, bm, bn, wgs, cus, 0, kNumXcd)
+             ? 1
+             : 0;
+}
+
+// The last shapes whose walk was counted (the count walks up to 64 list entries per CU and costs
+// up to ~75 us on the host; a serving loop repeats few shapes). A small ring under a mutex.
+struct CausalWalkCache {
+  struct Entry {
+    int64_t n = -1, bh = -1;
+    int bm = 0, bn = 0, wgs = 0, cus = 0, walk = 0;
+  };
+  static constexpr int kSlots = 16;
+  std::mutex mu;
+  Entry slot[kSlots];
+  int next = 0;
+};
+inline CausalWalkCache& causal_walk_cache() {
+  static CausalWalkCache cache;
+  return cache;
+}
+
 // The walk for causal rows. wgs: workgroups per XCD of the persistent launch, cus: CUs per XCD.
 // per_xcd: whether the per-XCD lists may be used (the launcher's heads rule); rank_only: no
 // head-by-head lists (d = 64). Beyond 64 blocks per CU, where a pass's pattern averages out over
@@ -69,9 +94,17 @@ inline int causal_walk(int64_t n, int64_t bh, int bm, int bn, int wgs, int cus, 
   if (rank_only) return 1;
   const long long nq = (n + bm - 1) / bm, heads = (bh + kNumXcd - 1) / kNumXcd;
   if (wgs <= 0 || cus <= 0 || heads * nq > 64LL * cus) return 0;
-  return causal_walk_busiest(n, bh, bm, bn, wgs, cus, 1, kNumXcd) < causal_walk_busiest(n, bh, bm, bn, wgs, cus, 0, kNumXcd)
-             ? 1
-             : 0;
+  CausalWalkCache& c = causal_walk_cache();
+  {
+    std::lock_guard<std::mutex> lock(c.mu);
+    for (const auto& e : c.slot)
+      if (e.n == n && e.bh == bh && e.bm == bm && e.bn == bn && e.wgs == wgs && e.cus == cus) return e.walk;
+  }
+  const int walk = causal_walk_uncached(n, bh, bm, bn, wgs, cus);   // counted outside the lock
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.slot[c.next] = CausalWalkCache::Entry{n, bh, bm, bn, wgs, cus, walk};
+  c.next = (c.next + 1) % CausalWalkCache::kSlots;
+  return walk;
 }
 
 }  // namespace pa

@@ -369,7 +369,8 @@ hipError_t launch_tiled(const void* q, const void* k, const void* v, void* o, fl
   else if (n <= 2048) hipLaunchKernelGGL(pa::tiled_softmax_rows<32>, sm_grid, dim3(256), 0, stream, s, n);
   else if (n <= 4096) hipLaunchKernelGGL(pa::tiled_softmax_rows<64>, sm_grid, dim3(256), 0, stream, s, n);
   else if (n <= 8192) hipLaunchKernelGGL(pa::tiled_softmax_rows<128>, sm_grid, dim3(256), 0, stream, s, n);
-  else hipLaunchKernelGGL(pa::tiled_softmax, sm_grid, dim3(256), 0, stream, s, n);
+  else if (n <= 16384) hipLaunchKernelGGL(pa::tiled_softmax_segments<64>, dim3(n, bh), dim3(256), 0, stream, s, n);
+  else hipLaunchKernelGGL(pa::tiled_softmax_segments<128>, dim3(n, bh), dim3(256), 0, stream, s, n);
   bool mfma_pv = false;
   if constexpr (std::is_same<T, pa::f16>::value) {
     // fp16 V with d in {64, 128}, 16-byte aligned rows of P (N a multiple of 4) and V, one head's

@@ -154,9 +154,13 @@ def fused_db(q, k, v, causal=False):
 def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False, *,
              out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """v4: both matmuls on MFMA (fp16/bf16 in, fp32 accumulate), online softmax in between.
-    FP16 or BF16, d in {64, 128}. Non-causal d=128 calls with an even number of 64-key tiles run the
-    persistent launch (PA_PERSISTENT=0 in the environment when the library loads, or
-    cuda_attn._native.set_persistent(False), selects the per-block one; same bits)."""
+    FP16 or BF16, d in {64, 128}. The library picks the launch from the shape: persistent (as many
+    workgroups as fit at once, walking the query blocks) for every causal call and for non-causal
+    calls with an even number of 64-key tiles or an odd number, above one, of full ones; a key split
+    for short d = 64 rows on a small grid; otherwise one workgroup per query block.
+    cuda_attn._native.fused_tc_kernel names the launch a call takes. PA_PERSISTENT=0 in the
+    environment when the library loads, or cuda_attn._native.set_persistent(False), selects one
+    workgroup per query block instead of the persistent launch (same bits)."""
     _checks.check_inputs(q, k, v)
     _checks.check_tc(q, k, v)
     od = _checks.resolve_out_dtype("fused_tc", q, out_dtype)

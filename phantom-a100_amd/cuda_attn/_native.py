@@ -93,5 +93,7 @@ def fused_tc_kernel(dtype: int, out_dtype: int, bh: int, n: int, d: int, causal:
 
 
 def set_persistent(enable: bool) -> bool:
-    """Switch fused_tc's persistent d=128 launch on or off; returns the previous setting."""
+    """Switch fused_tc's persistent launch on or off (every shape that would take it: causal calls,
+    and non-causal ones with an even number of 64-key tiles or an odd number, above one, of full
+    ones, at d = 64 and 128); returns the previous setting. fused_tc_kernel names the launch."""
     return bool(lib().pa_set_persistent(int(bool(enable))))

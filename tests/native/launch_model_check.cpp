@@ -91,6 +91,16 @@ int main() {
     CHECK(h == k.by_head && r == k.by_rank, "B*H=%d N=%d d=%d: busiest %lld / %lld, expected %lld / %lld", k.bh, k.n,
           k.d, h, r, k.by_head, k.by_rank);
     CHECK(walk == k.walk, "B*H=%d N=%d d=%d: walk %d, expected %d", k.bh, k.n, k.d, walk, k.walk);
+    // The second call of a shape comes from the walk cache and must agree.
+    CHECK(pa::causal_walk(k.n, k.bh, bm, bn, wgs, cus, k.d == 64, true) == walk, "B*H=%d N=%d: cached walk differs",
+          k.bh, k.n);
+  }
+  // More shapes than the cache holds, then the first again: evicted entries are counted afresh.
+  for (int i = 0; i < 40; ++i) {
+    const int n = 1024 + 64 * i, wgs = 32;
+    const int want = pa::causal_walk_uncached(n, 128, 256, 64, wgs, 32);
+    CHECK(pa::causal_walk(n, 128, 256, 64, wgs, 32, false, true) == want, "N=%d: walk differs from the count", n);
+    CHECK(pa::causal_walk(n, 128, 256, 64, wgs, 32, false, true) == want, "N=%d: cached walk differs", n);
   }
   // Heads the per-XCD lists may not take walk one list over the device.
   CHECK(pa::causal_walk(16384, 4, 256, 64, 8, 32, false, false) == 2, "B*H=4: walk not the device list");

@@ -32,6 +32,7 @@ from cuda_attn.workloads import CONFIGS, config_inputs, make_qkv
 pytestmark = pytest.mark.gpu
 
 TOL = {torch.float32: 1e-4, torch.float16: 2e-3}   # /root/reference/tests/test_correctness.py:12
+F32_BAR = 1e-5   # fp32 inputs against float64: the bar the configurations are held to
 SHAPES_N = [1, 15, 16, 63, 64, 65, 128, 512, 1000, 1024, 2048]
 ALL = list(cuda_attn.KERNELS)
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
@@ -87,6 +88,11 @@ def test_matches_reference(name, dtype, n, causal):
     assert out.shape == q.shape and out.dtype == dtype
     err = max_err(out, cuda_attn.reference(q, k, v, causal))
     assert err <= TOL[dtype], f"max abs error {err:.2e} > {TOL[dtype]:.0e}"
+    if dtype == torch.float32:
+        # fp32 inputs: the 1e-5 bar against float64 as well (the fp32 SDPA above carries fp32
+        # rounding of its own, which is why the reference's bar against it is 1e-4)
+        err64 = max_err(out.double(), f64_reference_gpu(q, k, v, causal))
+        assert err64 <= F32_BAR, f"max abs error vs float64 {err64:.2e} > {F32_BAR:.0e}"
 
 
 @pytest.mark.parametrize("br,bc", [(64, 32), (64, 64), (128, 32), (128, 64)])
@@ -118,9 +124,46 @@ def test_long_sequence_fused_versions_agree():
 
 @pytest.mark.parametrize("name", ["naive", "tiled"])
 @pytest.mark.parametrize("d", [32, 80, 128])
-def test_other_head_dims_for_unfused(name, d):
+@pytest.mark.parametrize("causal", [False, True])
+def test_other_head_dims_for_unfused(name, d, causal):
     q, k, v = gpu_qkv(1, 2, 200, d, torch.float32)
-    assert max_err(cuda_attn.KERNELS[name](q, k, v), cuda_attn.reference(q, k, v)) <= 1e-4
+    out = cuda_attn.KERNELS[name](q, k, v, causal)
+    assert max_err(out, cuda_attn.reference(q, k, v, causal)) <= 1e-4
+    assert max_err(out.double(), f64_reference_gpu(q, k, v, causal)) <= F32_BAR
+
+
+def f64_rows(q, k, v, rows, causal):
+    """float64 softmax(QK^T/sqrt(d))V for the given query rows of every head."""
+    b, h, n, d = q.shape
+    idx = torch.as_tensor(rows, device=q.device)
+    qs = q.reshape(b * h, n, d)[:, idx].double()
+    s = torch.matmul(qs, k.reshape(b * h, n, d).double().transpose(1, 2).contiguous()) / np.sqrt(d)
+    if causal:
+        keys = torch.arange(n, device=q.device)
+        s.masked_fill_(keys[None, None, :] > idx[None, :, None], float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v.reshape(b * h, n, d).double())
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 8320, 64), (1, 2, 9000, 80), (1, 1, 20000, 64), (1, 1, 33000, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_tiled_long_rows(shape, dtype, causal):
+    """tiled rows longer than the one-wave softmax holds (N > 8192): one workgroup per row, in
+    one register-held segment up to N = 32768 and in several beyond, against float64 on sampled
+    rows (the first, those around a 64-row tile edge, the middle, the last and random ones)."""
+    b, h, n, d = shape
+    print(f"[tiled long] {shape} {dtype} causal={causal}", flush=True)
+    q, k, v = gpu_qkv(b, h, n, d, dtype, seed=11)
+    out = cuda_attn.tiled(q, k, v, causal)
+    torch.cuda.synchronize()
+    gen = np.random.default_rng(n)
+    rows = sorted({0, 1, 63, 64, 65, n // 2, n - 2, n - 1, *gen.integers(0, n, 24).tolist()})
+    ref = f64_rows(q, k, v, rows, causal)
+    got = out.reshape(b * h, n, d)[:, torch.as_tensor(rows, device=q.device)].double()
+    bar = F32_BAR if dtype == torch.float32 else 2e-3
+    err = (got - ref).abs().max().item()
+    assert np.isfinite(err) and err <= bar, f"max abs error {err:.2e} > {bar:.0e}"
 
 
 @pytest.mark.parametrize("d", [32, 64, 80, 96, 128])
