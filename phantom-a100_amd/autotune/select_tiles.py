@@ -6,7 +6,10 @@
 
 Replaces the reference's simulator-driven loop (/root/reference/autotune/hw_counters.py,
 diagnose.py) with measurements on the device. For every compiled candidate of the entry point
-(fused_tuned: (br, bc) x {one, two} LDS stages; fused_tc: its compiled tile) the tool
+(fused_tuned: (br, bc) x {one, two} LDS stages; fused_tc: its shipped tile in both launch forms,
+persistent and one workgroup per query block, plus the alternatives of libphantom_attn_tiles.so at
+the same dtype and head dim: other query rows per workgroup, keys per tile, LDS stages and
+workgroups per CU) the tool
   1. gates the output against a float64 reference (failing candidates are reported, not timed),
   2. times it with the flushing protocol of bench/benchmark.py,
   3. with --profile, runs bench/run_one.py under rocprofv3 (one kernel trace, then one run per
@@ -39,6 +42,7 @@ from cuda_attn.workloads import attention_flops, compulsory_bytes  # noqa: E402
 
 from autotune import diagnose as dg  # noqa: E402
 from autotune import hw_counters as hc  # noqa: E402
+from autotune import tile_candidates as tc  # noqa: E402
 
 RUN_ONE = os.path.join(_PKG, "bench", "run_one.py")
 RESOURCES = os.path.join(_PKG, "cuda_attn", "kernel_resources.json")
@@ -48,13 +52,24 @@ MANGLED_T = {torch.float16: "DF16_", torch.bfloat16: "DF16b", torch.float32: "f"
 TC_TILE = {64: (128, 64, 2), 128: (256, 64, 2)}
 
 
-def candidates(entry: str, d: int):
-    """(label, br, bc, stages) of every compiled configuration of `entry` at head dim d."""
+SHIPPED, PER_BLOCK = "shipped", "per_block"
+
+
+def candidates(entry: str, d: int, dtype: torch.dtype | None = None, with_alternatives: bool = True):
+    """(label, br, bc, stages, source) of every compiled configuration of `entry` at head dim d.
+    source: "tuned" (fused_tuned), SHIPPED (fused_tc as launched), PER_BLOCK (fused_tc's tile with
+    the persistent launch switched off), or the index of an alternative in libphantom_attn_tiles.so
+    (those of the dtype, when the library is built and with_alternatives is set)."""
     if entry == "fused_tuned":
-        return [(f"br{br}_bc{bc}_{'db' if db else 'sb'}", br, bc, 2 if db else 1)
+        return [(f"br{br}_bc{bc}_{'db' if db else 'sb'}", br, bc, 2 if db else 1, "tuned")
                 for br, bc in _checks.TUNED_CONFIGS for db in (False, True)]
     br, bc, st = TC_TILE[d]
-    return [(f"br{br}_bc{bc}_{st}stage", br, bc, st)]
+    out = [(f"br{br}_bc{bc}_{st}stage", br, bc, st, SHIPPED),
+           (f"br{br}_bc{bc}_{st}stage_per_block", br, bc, st, PER_BLOCK)]
+    if with_alternatives and tc.available():
+        out += [(c["label"], c["br"], c["bc"], c["stages"], c["index"]) for c in tc.candidates()
+                if c["d"] == d and (dtype is None or c["dtype"] == dtype)]
+    return out
 
 
 def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dtype: torch.dtype,
@@ -65,15 +80,23 @@ def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dt
             f"Li{ksplit}ELb{int(persistent)}ELb{int(ragged)}ELb{int(causal)}EE")
 
 
-def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal: bool, br: int) -> dict:
+def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal: bool, br: int,
+                source="shipped") -> dict:
     """How the library launches this call: the key split, persistent and ragged flags and the
-    number of workgroups, read from the launcher's own description (pa_fused_tc_kernel), so the
-    report names the kernel that actually runs."""
+    number of workgroups, read from the launcher's own description (pa_fused_tc_kernel, or
+    pa_tiles_kernel for an alternative), so the report names the kernel that actually runs."""
     if entry != "fused_tc":
         return {"ksplit": 1, "persistent": False, "ragged": False, "causal": False, "workgroups": -(-n // br) * bh,
                 "description": ""}
-    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
-    desc = _native.fused_tc_kernel(code, code, bh, n, d, causal)
+    if isinstance(source, int):
+        desc = tc.kernel(source, bh, n)
+    else:
+        code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+        prev = _native.set_persistent(source != PER_BLOCK)
+        try:
+            desc = _native.fused_tc_kernel(code, code, bh, n, d, causal)
+        finally:
+            _native.set_persistent(prev)
     grid = re.search(r"grid (\d+) x", desc)
     return {"ksplit": 2 if "key split 2" in desc else 1, "persistent": ", persistent" in desc,
             "ragged": ", ragged" in desc, "causal": ", persistent, causal" in desc,
@@ -94,27 +117,45 @@ def find_resources(res: dict, key: str) -> dict | None:
     return None
 
 
-def make_call(entry, q, k, v, causal, br, bc, stages, out_dtype=None):
+def make_call(entry, q, k, v, causal, br, bc, stages, out_dtype=None, source=SHIPPED):
     if entry == "fused_tuned":
         return lambda: cuda_attn.fused_tuned(q, k, v, causal, stages == 2, br, bc, out_dtype=out_dtype)
+    if isinstance(source, int):   # an alternative: output in the input dtype only
+        return lambda: tc.forward(source, q, k, v, causal)
+    if source == PER_BLOCK:
+        def per_block():
+            prev = _native.set_persistent(False)
+            try:
+                return cuda_attn.fused_tc(q, k, v, causal, out_dtype=out_dtype)
+            finally:
+                _native.set_persistent(prev)
+        return per_block
     return lambda: cuda_attn.fused_tc(q, k, v, causal, out_dtype=out_dtype)
 
 
-def float64_error(q, k, v, out, causal) -> float:
+def float64_error(q, k, v, out, causal) -> tuple[float, float]:
+    """Max abs error against float64 on the first and last head, and half an ulp of the output
+    dtype at the largest reference value (the output's own rounding, 0 for fp32 outputs)."""
     b, h, n, d = q.shape
     heads = sorted({0, b * h - 1})
     qh, kh, vh, oh = (t.reshape(b * h, n, d)[heads].double() for t in (q, k, v, out.float()))
     s = torch.matmul(qh, kh.transpose(1, 2).contiguous()) / d ** 0.5
     if causal:
         s = s.masked_fill(torch.ones(n, n, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
-    return (oh - torch.matmul(torch.softmax(s, -1), vh)).abs().max().item()
+    ref = torch.matmul(torch.softmax(s, -1), vh)
+    rounding = 0.0 if out.dtype == torch.float32 else 0.5 * torch.finfo(out.dtype).eps * ref.abs().max().item()
+    return (oh - ref).abs().max().item(), rounding
 
 
-def profile_candidate(args, br, bc, stages, out_dir) -> dict:
+def profile_candidate(args, br, bc, stages, out_dir, source="tuned", label="") -> dict:
     """Kernel trace + counter passes of one candidate; returns the aggregated quantities."""
     cmd = [sys.executable, RUN_ONE, "--impl", args.entry, "--n", str(args.n), "--batch", str(args.batch),
            "--heads", str(args.heads), "--dim", str(args.dim), "--dtype", args.dtype, "--reps", "3",
            "--br", str(br), "--bc", str(bc), "--db", str(1 if stages == 2 else 0), "--calibrate"]
+    if isinstance(source, int):
+        cmd += ["--candidate", label]
+    elif source == PER_BLOCK:
+        cmd.append("--per-block")
     if args.causal:
         cmd.append("--causal")
     tr = hc.run_pass(cmd, None, out_dir, "trace", timeout=args.pass_timeout)
@@ -151,22 +192,27 @@ def evaluate(args) -> list[dict]:
     flops = attention_flops(args.batch, args.heads, args.n, args.dim, args.causal)
     comp = compulsory_bytes(args.batch * args.heads, args.n, args.dim, dt, dt)
     rows = []
-    for label, br, bc, st in candidates(args.entry, args.dim):
+    only = set(args.only.split(",")) if args.only else None
+    for label, br, bc, st, source in candidates(args.entry, args.dim, dt, with_alternatives=not args.shipped_only):
+        if only is not None and label not in only:
+            continue
         row = {"candidate": label, "br": br, "bc": bc, "stages": st}
-        fn = make_call(args.entry, q, k, v, args.causal, br, bc, st)
-        try:   # gate on fp32 output so the 2e-3 bar does not include the output's own rounding
-            err = float64_error(q, k, v, make_call(args.entry, q, k, v, args.causal, br, bc, st, torch.float32)(),
-                                args.causal)
+        fn = make_call(args.entry, q, k, v, args.causal, br, bc, st, source=source)
+        try:   # gate on fp32 output where the candidate has one, so the 2e-3 bar does not include
+            # the output's own rounding; the alternatives (input-dtype output) get that rounding on top
+            out = make_call(args.entry, q, k, v, args.causal, br, bc, st,
+                            None if isinstance(source, int) else torch.float32, source)()
+            err, rounding = float64_error(q, k, v, out, args.causal)
         except RuntimeError as e:
             rows.append(dict(row, status="skipped: " + str(e).splitlines()[0][:80]))
             continue
         row["max_abs_err"] = err
-        if not err <= 2e-3:
+        if not err <= 2e-3 + rounding:
             rows.append(dict(row, status="wrong_result"))
             continue
         med, p10, p90 = time_calls(fn, 5, args.iters, flush)
         row.update(status="ok", median_ms=med, p10_ms=p10, p90_ms=p90, tflops=flops / (med * 1e-3) / 1e12)
-        form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br)
+        form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br, source)
         res = find_resources(res_all, kernel_key(dt, args.dim, br, bc, st, dt, form["ksplit"], form["persistent"],
                                                  form["ragged"], form["causal"]))
         row["launch"] = form["description"]
@@ -178,10 +224,10 @@ def evaluate(args) -> list[dict]:
             row["resident_wgs_per_cu"] = dg.resident_wgs_per_cu(waves, threads)
         row["workgroups"] = form["workgroups"]
         if args.profile and args.profile_dir:      # keep the raw rocprofv3 output per candidate
-            prof = profile_candidate(args, br, bc, st, os.path.join(args.profile_dir, label))
+            prof = profile_candidate(args, br, bc, st, os.path.join(args.profile_dir, label), source, label)
         elif args.profile:
             with tempfile.TemporaryDirectory() as tmp:
-                prof = profile_candidate(args, br, bc, st, tmp)
+                prof = profile_candidate(args, br, bc, st, tmp, source, label)
         if args.profile:
             for kk, vv in prof.items():
                 if vv is not None:
@@ -248,6 +294,9 @@ def parse_args(argv=None):
     p.add_argument("--profile", action="store_true", help="collect rocprofv3 counters for every candidate")
     p.add_argument("--profile-dir", default=None, help="keep the raw rocprofv3 output here (default: a temporary directory)")
     p.add_argument("--pass-timeout", type=int, default=120)
+    p.add_argument("--shipped-only", action="store_true",
+                   help="fused_tc: only the shipped tile (both launch forms), not the alternatives")
+    p.add_argument("--only", default="", help="comma-separated candidate labels to evaluate (default: all)")
     p.add_argument("--out", default=None, help="write the markdown report here (and <out>.json)")
     a = p.parse_args(argv)
     if a.entry == "fused_tuned" and (a.dim != 64 or a.dtype != "fp16"):

@@ -21,6 +21,12 @@ DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
 
 
 def make_call(a, q, k, v):
+    if a.candidate:   # an alternative tile of fused_tc (libphantom_attn_tiles.so)
+        from autotune import tile_candidates as tc
+        index = {c["label"]: c["index"] for c in tc.candidates()}
+        if a.candidate not in index:
+            raise SystemExit(f"no candidate {a.candidate!r}; compiled: {sorted(index)}")
+        return lambda: tc.forward(index[a.candidate], q, k, v, a.causal)
     if a.impl == "fused_tuned":
         return lambda: cuda_attn.fused_tuned(q, k, v, a.causal, bool(a.db), a.br, a.bc)
     fn = cuda_attn.KERNELS[a.impl]
@@ -40,9 +46,15 @@ def main(argv=None):
     p.add_argument("--bc", type=int, default=32)
     p.add_argument("--db", type=int, default=1)
     p.add_argument("--reps", type=int, default=5)
+    p.add_argument("--candidate", default="", help="fused_tc: run this alternative of libphantom_attn_tiles.so")
+    p.add_argument("--per-block", action="store_true",
+                   help="fused_tc: one workgroup per query block (the persistent launch switched off)")
     p.add_argument("--calibrate", action="store_true",
                    help="first copy 1 GiB device-to-device: a known-size transfer that calibrates FETCH_SIZE")
     a = p.parse_args(argv)
+    if a.per_block:
+        from cuda_attn import _native
+        _native.set_persistent(False)
     if a.calibrate:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -56,7 +68,8 @@ def main(argv=None):
     for _ in range(a.reps):
         fn()
     torch.cuda.synchronize()
-    print(f"ran {a.impl} N={a.n} d={a.dim} {a.dtype} x{a.reps}", flush=True)
+    print(f"ran {a.impl}{' ' + a.candidate if a.candidate else ''}{' per block' if a.per_block else ''} "
+          f"N={a.n} d={a.dim} {a.dtype} x{a.reps}", flush=True)
 
 
 if __name__ == "__main__":

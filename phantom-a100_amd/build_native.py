@@ -26,8 +26,12 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "cuda_attn", "libphantom_attn.so")
+# The tile alternatives for the counter-driven tile choice (autotune/select_tiles.py); never loaded
+# by cuda_attn.
+TILES_OUT = os.path.join(HERE, "cuda_attn", "libphantom_attn_tiles.so")
 RESOURCES = os.path.join(HERE, "cuda_attn", "kernel_resources.json")
-SOURCES = ["pa_attn.hip"]
+LIBRARIES = {OUT: ["pa_attn.hip"], TILES_OUT: ["pa_tiles.hip"]}
+SOURCES = [src for srcs in LIBRARIES.values() for src in srcs]
 ARCH = "gfx950"
 
 DEVICE_FLAGS = [
@@ -46,8 +50,9 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every source and link libphantom_attn.so; returns its path."""
-    objs = []
+    """Compile every source (in parallel) and link libphantom_attn.so and libphantom_attn_tiles.so;
+    returns the path of libphantom_attn.so."""
+    objs = {}
     os.makedirs(os.path.join(HERE, "_build"), exist_ok=True)
     procs = []
     for src in SOURCES:
@@ -57,7 +62,7 @@ def build(verbose: bool = False) -> str:
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
-        objs.append(obj)
+        objs[src] = obj
     failed = []
     resources = {}
     for src, p in procs:
@@ -75,11 +80,12 @@ def build(verbose: bool = False) -> str:
             print("\n".join(lines))
     if failed:
         raise RuntimeError("hipcc failed for: " + ", ".join(failed))
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
-    subprocess.run(cmd, check=True)
-    check_no_missing_stubs(tmp)
-    os.replace(tmp, OUT)
+    for lib_path, srcs in LIBRARIES.items():
+        tmp = lib_path + ".tmp"
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *(objs[src] for src in srcs), "-o", tmp]
+        subprocess.run(cmd, check=True)
+        check_no_missing_stubs(tmp)
+        os.replace(tmp, lib_path)
     with open(RESOURCES, "w") as fh:
         json.dump(resources, fh, indent=1, sort_keys=True)
         fh.write("\n")

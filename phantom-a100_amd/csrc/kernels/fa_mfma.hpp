@@ -105,13 +105,14 @@ struct MfmaLds {
 };
 
 // The persistent forms' O staging rows: each wave stages its 32 rows of O in ROWS-row passes that
-// fit LIMIT bytes per workgroup (three d = 64 workgroups per CU: 3 x (32 + 16) KB; one d = 128
-// workgroup: 64 + 64 KB), so BYTES of LDS per workgroup beside the K/V stages.
+// fit LIMIT bytes per workgroup (three d = 64 workgroups per CU: 3 x (32 + 16) KB; one 256-query
+// d = 128 workgroup: 64 + 64 KB; two 128-query d = 128 workgroups: 2 x (64 + 16) KB), so BYTES of
+// LDS per workgroup beside the K/V stages.
 template <int D, int BM, typename OutT>
 struct MfmaOStage {
   static constexpr int ROW = D * (int)sizeof(OutT);       // bytes of one O row
   static constexpr int CHUNKS = ROW / 16;                  // its 16-byte chunks
-  static constexpr int LIMIT = D == 64 ? 16384 : 65536;
+  static constexpr int LIMIT = (D == 64 || BM < 256) ? 16384 : 65536;
   static constexpr int PASSES = (BM * ROW + LIMIT - 1) / LIMIT;
   static constexpr int ROWS = 32 / PASSES;                 // rows of a wave per pass
   static constexpr int BYTES = BM / 32 * ROWS * ROW;

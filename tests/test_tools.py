@@ -6,6 +6,7 @@ from __future__ import annotations
 
 import importlib.util
 import os
+import re
 import sys
 
 import pytest
@@ -19,6 +20,7 @@ sys.path.insert(0, PKG)
 from autotune import diagnose as dg  # noqa: E402
 from autotune import hw_counters as hc  # noqa: E402
 from autotune import select_tiles as st  # noqa: E402
+from cuda_attn import _native  # noqa: E402
 
 
 def load(name, path):
@@ -265,7 +267,43 @@ def test_candidates_name_compiled_kernels():
     assert st.find_resources(res, st.kernel_key(torch.bfloat16, 128, 256, 64, 2, torch.bfloat16, persistent=True))
     assert not st.find_resources(res, st.kernel_key(torch.bfloat16, 128, 256, 64, 2, torch.bfloat16))
     assert len(st.candidates("fused_tuned", 64)) == 8
-    assert st.candidates("fused_tc", 128) == [("br256_bc64_2stage", 256, 64, 2)]
+    assert st.candidates("fused_tc", 128, with_alternatives=False) == [
+        ("br256_bc64_2stage", 256, 64, 2, st.SHIPPED), ("br256_bc64_2stage_per_block", 256, 64, 2, st.PER_BLOCK)]
+
+
+def test_tile_alternatives_library_without_gpu():
+    """libphantom_attn_tiles.so loads, exports what its header declares, lists at least three
+    alternatives per fused_tc head dim (none of them the shipped tile) with distinct labels, and
+    rejects calls it does not compile before any HIP call."""
+    import ctypes
+    from autotune import tile_candidates as tc
+    header = os.path.join(os.path.dirname(HERE), "include", "phantom_attn_tiles.h")
+    text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(pa_[a-z0-9_]+)\s*\(", text)))
+    assert declared == sorted(tc.PROTOTYPES)
+    for name in declared:
+        assert ctypes.cast(getattr(tc.lib(), name), ctypes.c_void_p).value, name
+    cands = tc.candidates()
+    assert len({c["label"] for c in cands}) == len(cands)
+    for d, dtype in ((128, torch.bfloat16), (64, torch.float16)):
+        alts = [c for c in cands if c["d"] == d and c["dtype"] == dtype]
+        assert len(alts) >= 3, d
+        shipped = st.TC_TILE[d]
+        assert all((c["br"], c["bc"], c["stages"]) != shipped or not c["persistent"] for c in alts)
+        rows = st.candidates("fused_tc", d, dtype)
+        assert rows[0][4] == st.SHIPPED and len(rows) == 2 + len(alts)
+        assert [r[0] for r in rows[2:]] == [c["label"] for c in alts]
+    c0 = cands[0]
+    desc = tc.kernel(c0["index"], 128, 4096)
+    assert desc.startswith(f"fa_mfma_fwd<bf16, D={c0['d']}, BM={c0['br']}, BN={c0['bc']}") and "grid" in desc
+    lib, p = tc.lib(), ctypes.c_void_p(256)   # never dereferenced: validation fails first
+    rc = lib.pa_tiles_fwd(c0["index"], p, p, p, p, _native.DTYPE_BF16, 1, 4096, c0["d"], 1, None)
+    assert rc == _native.ERR_UNSUPPORTED and b"non-causal" in lib.pa_tiles_last_error()
+    rc = lib.pa_tiles_fwd(c0["index"], p, p, p, p, _native.DTYPE_F16, 1, 4096, c0["d"], 0, None)
+    assert rc == _native.ERR_UNSUPPORTED and b"compiled for" in lib.pa_tiles_last_error()
+    rc = lib.pa_tiles_fwd(len(cands), p, p, p, p, _native.DTYPE_BF16, 1, 4096, 128, 0, None)
+    assert rc == _native.ERR_INVALID
+    assert lib.pa_tiles_label(-1) == b""
 
 
 # ---------------------------------------------------------------- bottleneck rules
