@@ -270,6 +270,60 @@ def cpu_baseline(headline: str, target_s: float) -> dict:
     }
 
 
+class ClockSampler:
+    """Samples the GPU's shader clock (per XCD) and socket power with amdsmi on a background thread
+    while the steps run, so that the line's `frac` can be read against the clock the box ran at
+    (MI355X runs this load at its power cap; the clock differs from box to box). Inactive (the
+    line reports null) where amdsmi does not import or cannot read the device."""
+
+    def __init__(self, period_s: float = 0.005):
+        self.period, self.samples, self.error = period_s, [], None
+        self._stop, self._thread, self._smi, self._handle = False, None, None, None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self._smi, self._handle = amdsmi, amdsmi.amdsmi_get_processor_handles()[0]
+            self._smi.amdsmi_get_gpu_metrics_info(self._handle)
+        except Exception as e:   # noqa: BLE001 - any failure means no clock in the line
+            self._smi, self.error = None, f"{type(e).__name__}: {e}"[:200]
+
+    def _run(self):
+        while not self._stop:
+            t = time.perf_counter()
+            try:
+                m = self._smi.amdsmi_get_gpu_metrics_info(self._handle)
+                xcd = [int(c) for c in (m.get("current_gfxclks") or []) if isinstance(c, int) and 0 < c < 65535]
+                power = m.get("current_socket_power")
+                self.samples.append((t, xcd, power if isinstance(power, (int, float)) else None))
+            except Exception as e:   # noqa: BLE001
+                self.error = f"{type(e).__name__}: {e}"[:200]
+            time.sleep(self.period)
+
+    def start(self):
+        if self._smi is not None:
+            import threading
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def stop(self):
+        self._stop = True
+        if self._thread is not None:
+            self._thread.join()
+
+    def summary(self, t0: float, t1: float):
+        """Median per-XCD clock (MHz), their mean and min, and median socket power (W) of the samples
+        taken in [t0, t1]; None without samples."""
+        win = [s for s in self.samples if t0 <= s[0] <= t1 and s[1]]
+        if not win:
+            return None
+        nx = min(len(s[1]) for s in win)
+        per_xcd = [statistics.median(s[1][i] for s in win) for i in range(nx)]
+        powers = [s[2] for s in win if s[2] is not None]
+        return {"samples": len(win), "per_xcd_mhz": per_xcd, "mean_mhz": round(statistics.mean(per_xcd), 1),
+                "min_mhz": min(per_xcd), "socket_power_w": statistics.median(powers) if powers else None}
+
+
 def traffic_from_profile():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 PMC summary."""
     try:
@@ -329,9 +383,17 @@ def main():
         log("bench.py: correctness gate failed; not timing a wrong result")
         sys.exit(3)
 
+    clock = ClockSampler().start()
+    t_settle = time.perf_counter()
     st = settle(fn, args.settle)
     log(f"[settle] {st['calls']} calls in {st['seconds']} s before warm-up")
+    t_timed = time.perf_counter()
     ms_total, wall_ms = time_steps(fn, args.steps, args.warmup)
+    t_end = time.perf_counter()
+    clock.stop()
+    clk_timed = clock.summary(t_timed, t_end)
+    clk_settle = clock.summary(max(t_settle, t_timed - 1.0), t_timed)
+    log(f"[clock] warm-up + timed steps: {clk_timed}; last second of settle: {clk_settle}")
     ms_step = ms_total / args.steps
     flops = cfg.flops()
     value = flops * args.steps / (ms_total * 1e-3) / 1e12
@@ -353,6 +415,10 @@ def main():
                      "traffic": traffic_from_profile() if cfg.name == HEADLINE else None,
                      "kernel": kernel_description(cfg), "flops_per_launch": flops},
         "gate_max_abs_err": float(f"{err:.3e}"),
+        "clock": None if clk_timed is None and clk_settle is None else {
+            "source": "amdsmi gpu_metrics current_gfxclks (shader clock per XCD) and current_socket_power, "
+                      "sampled every 5 ms on a host thread",
+            "warmup_and_timed_steps": clk_timed, "last_second_of_settle": clk_settle},
         "library": _native.version(),
         "device": torch.cuda.get_device_name(0),
     }
