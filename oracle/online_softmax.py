@@ -165,7 +165,8 @@ def attention_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool =
 def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = False,
                            p_dtype: str | None = None, bc: int = 64, group: int = 32,
                            lazy_log2: float = 8.0, stats: dict | None = None,
-                           check: str = "max", two_term: bool = True) -> np.ndarray:
+                           check: str = "max", two_term: bool = True, shift: float | None = None,
+                           fire: float = 2.0) -> np.ndarray:
     """The fused MFMA kernel's arithmetic, in float32 (a model of this build, not the reference).
 
     Same log2-domain online softmax as ``attention_online``, with the two changes the kernel
@@ -180,10 +181,12 @@ def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: 
       * ``"max"`` (the fp16 kernels): the row max of each tile is compared with m before the
         exponentials, as above;
       * ``"rounded"`` (the bf16 kernel): the exponentials are taken against the reference
-        m_ref = m + (lazy_log2 - 1), i.e. P' = P 2^-(lazy_log2 - 1), rounded, and the rescale
-        fires when some rounded P' of the group reaches 2; then every row whose max grew takes
-        m_ref = max + lazy_log2 - 1, O and l are multiplied by 2^(m_ref_old - m_ref_new) and
-        P' is recomputed. A group's first tile always takes the exact max. m_ref starts at the
+        m_ref = m + shift (default lazy_log2 - 1), i.e. P' = P 2^-shift, rounded, and the rescale
+        fires when some rounded P' of the group reaches ``fire`` (default 2); then every row whose
+        max grew takes m_ref = max + shift, O and l are multiplied by 2^(m_ref_old - m_ref_new) and
+        P' is recomputed. The fp16 kernels' non-causal persistent forms (and d = 128 per block) use
+        the same rule with shift = 4 and fire = 2^14 (a packed fp16 max instead of the bf16
+        exponent bit). A group's first tile always takes the exact max. m_ref starts at the
         finite -3e38, so masked scores give P' = 0. With ``two_term`` (the kernel's rule), a
         group whose rows see at most ``bc`` keys (a single tile) takes P' as two rounded terms,
         hi = round(P') and lo = round(P' - hi), both multiplied into O and summed into l.
@@ -191,7 +194,8 @@ def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: 
     ``"rounded"``) and the number of rescales.
     """
     if check == "rounded":
-        return _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats, two_term)
+        shift = lazy_log2 - 1.0 if shift is None else shift
+        return _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, shift, fire, stats, two_term)
     if check != "max":
         raise ValueError(f"unknown check {check!r}")
     q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
@@ -240,14 +244,16 @@ def attention_kernel_model(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: 
     return out
 
 
-def _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats, two_term=True):
-    """``attention_kernel_model(check="rounded")``: the bf16 kernel's overflow-check variant."""
+def _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, shift, fire, stats, two_term=True):
+    """``attention_kernel_model(check="rounded")``: the kernels' check on the rounded P' (bf16: the
+    top exponent bit, P' >= 2 with shift 7; fp16: the packed max, P' >= 2^14 with shift 4)."""
     q32, k32, v32 = (np.asarray(x, dtype=np.float32) for x in (q, k, v))
     *batch, n, d = q32.shape
     out = np.empty_like(q32)
     scale_log2 = np.float32(LOG2E / np.sqrt(d))
     kt = np.swapaxes(k32, -1, -2)
-    shift = np.float32(lazy_log2 - 1.0)
+    shift = np.float32(shift)
+    fire_at = np.float32(fire)
     p_max, rescales = 0.0, 0
     for i0 in range(0, n, group):
         i1 = min(i0 + group, n)
@@ -270,7 +276,7 @@ def _kernel_model_rounded(q, k, v, causal, p_dtype, bc, group, lazy_log2, stats,
                     return round_to(np.exp2(s - ref[..., None]).astype(np.float32), p_dtype)
 
             p = exp_round(m_ref)
-            fire = np.any(p >= 2, axis=(-1, -2), keepdims=False) if t else np.ones(batch, bool)
+            fire = np.any(p >= fire_at, axis=(-1, -2), keepdims=False) if t else np.ones(batch, bool)
             alpha = np.ones_like(m_ref)
             if np.any(fire):
                 mrow = s.max(axis=-1) + shift

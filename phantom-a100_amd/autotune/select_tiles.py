@@ -73,11 +73,12 @@ def candidates(entry: str, d: int, dtype: torch.dtype | None = None, with_altern
 
 
 def kernel_key(dtype: torch.dtype, d: int, br: int, bc: int, stages: int, out_dtype: torch.dtype,
-               ksplit: int = 1, persistent: bool = False, ragged: bool = False, causal: bool = False) -> str:
+               ksplit: int = 1, persistent: bool = False, ragged: bool = False, causal: bool = False,
+               check: bool = False) -> str:
     """Fragment of the mangled name of
-    pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT, PERSIST, RAGGED, CAUSAL>."""
+    pa::fa_mfma_fwd<T, D, BM, BN, STAGES, OutT, KSPLIT, PERSIST, RAGGED, CAUSAL, CHECK>."""
     return (f"fa_mfma_fwdI{MANGLED_T[dtype]}Li{d}ELi{br}ELi{bc}ELi{stages}E{MANGLED_T[out_dtype]}"
-            f"Li{ksplit}ELb{int(persistent)}ELb{int(ragged)}ELb{int(causal)}EE")
+            f"Li{ksplit}ELb{int(persistent)}ELb{int(ragged)}ELb{int(causal)}ELb{int(check)}EE")
 
 
 def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal: bool, br: int,
@@ -86,8 +87,8 @@ def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal:
     number of workgroups, read from the launcher's own description (pa_fused_tc_kernel, or
     pa_tiles_kernel for an alternative), so the report names the kernel that actually runs."""
     if entry != "fused_tc":
-        return {"ksplit": 1, "persistent": False, "ragged": False, "causal": False, "workgroups": -(-n // br) * bh,
-                "description": ""}
+        return {"ksplit": 1, "persistent": False, "ragged": False, "causal": False, "check": False,
+                "workgroups": -(-n // br) * bh, "description": ""}
     if isinstance(source, int):
         desc = tc.kernel(source, bh, n)
     else:
@@ -98,8 +99,11 @@ def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal:
         finally:
             _native.set_persistent(prev)
     grid = re.search(r"grid (\d+) x", desc)
+    # fp16 two-stage fused_tc tiles on non-causal rows use the packed-max check in the persistent
+    # forms and at d = 128 per block (the launcher names it); the fp16 two-stage alternatives always
+    check = ", packed-max check" in desc or (isinstance(source, int) and dtype == torch.float16 and "2 stages" in desc)
     return {"ksplit": 2 if "key split 2" in desc else 1, "persistent": ", persistent" in desc,
-            "ragged": ", ragged" in desc, "causal": ", persistent, causal" in desc,
+            "ragged": ", ragged" in desc, "causal": ", persistent, causal" in desc, "check": check,
             "workgroups": int(grid.group(1)) if grid else -(-n // br) * bh, "description": desc}
 
 
@@ -214,7 +218,7 @@ def evaluate(args) -> list[dict]:
         row.update(status="ok", median_ms=med, p10_ms=p10, p90_ms=p90, tflops=flops / (med * 1e-3) / 1e12)
         form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br, source)
         res = find_resources(res_all, kernel_key(dt, args.dim, br, bc, st, dt, form["ksplit"], form["persistent"],
-                                                 form["ragged"], form["causal"]))
+                                                 form["ragged"], form["causal"], form["check"]))
         row["launch"] = form["description"]
         threads = br // 32 * 64 * form["ksplit"]   # one wave per 32 query rows per key group
         if res:

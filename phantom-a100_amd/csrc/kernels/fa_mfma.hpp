@@ -37,16 +37,18 @@
 //    so rows are unpadded and 16-byte chunks are XOR-swizzled per row instead: the K operand
 //    reads (ds_read_b128, 16 consecutive rows at one column) and the transposed V reads
 //    (4 rows x 4 chunks per 32 lanes) each touch all 64 banks once.
-//  * STAGES == 2 (default): software pipeline inside each wave. For fp16, iteration t runs
+//  * STAGES == 2 (default): software pipeline inside each wave. For fp16 (causal rows, key split
+//    and the fused_tuned tiles), iteration t runs
 //        phase A: MFMAs of S(t+1) = K(t+1).Q^T   interleaved with the VALU work that turns S(t)
 //                                                 into P(t) (exp2, rounding; at d = 64 only its
 //                                                 second half)
 //        phase B: MFMAs of O += V(t)^T.P(t)^T    interleaved with the row sum of P(t), the row
 //                                                 max of S(t+1) and, at d = 64, the first half
 //                                                 of P(t+1)
-//    For bf16 the row max leaves the fast path: P is computed against the stale reference
-//    max and checked for overflow past 2^8 with one OR over its packed bf16 patterns (see the
-//    bf16 branch below), and the exponentials are split evenly over the two phases (the second
+//    For bf16, and for the fp16 fused_tc tiles on non-causal rows (CHECK), the row max leaves the
+//    fast path: P is computed against the stale reference max and checked afterwards, bf16 for
+//    overflow past 2^8 with one OR over its packed patterns, fp16 for reaching 2^14 with a packed
+//    max (see the branch below), and the exponentials are split evenly over the two phases (the second
 //    half of P(t) in phase A, the first half of P(t+1) in phase B), so each MFMA phase carries
 //    about the same VALU work.
 //    The interleave is fixed with scheduling-group barriers on a branch-free fast path (tile
@@ -130,20 +132,24 @@ template <int CR> __device__ __forceinline__ int v_swz(int row) { return CR == 1
 // forms 169-171 (held to 168 they spill 1-2 VGPRs and still run 3.5-6 % faster), the bf16 causal
 // form 193 (held to 168 it spills 10 VGPRs and runs 4-26 % faster: B*H x N = 256 x 512 404 -> 422,
 // 128 x 1024 516 -> 584, 128 x 2048 641 -> 794, 64 x 4096 692 -> 873, 16 x 8192 713 -> 887
-// TFLOP/s).
+// TFLOP/s); the fp16 persistent forms with the packed-max check (CHECK) take 169-171 and are held
+// to 168 (1 VGPR spilled; the ragged one 21).
 #ifndef PA_MFMA_MIN_WAVES
 #define PA_MFMA_MIN_WAVES 0
 #endif
-template <typename T, int D, bool PERSIST, bool RAGGED, bool CAUSAL>
+template <typename T, int D, bool PERSIST, bool RAGGED, bool CAUSAL, bool CHECK>
 constexpr int mfma_min_waves() {
   return PA_MFMA_MIN_WAVES > 0 ? PA_MFMA_MIN_WAVES
-                               : (PERSIST && D == 64 && (std::is_same<T, bf16>::value || RAGGED || CAUSAL)) ? 3 : 1;
+                               : (PERSIST && D == 64 && (std::is_same<T, bf16>::value || RAGGED || CAUSAL || CHECK)) ? 3 : 1;
 }
 
+// CHECK (fp16, two stages, no key split, not the causal form): the lazy rescale is triggered by a
+// check on the computed P' (as the bf16 kernels always do) instead of the row max of S before the
+// exponentials; see the branch below.
 template <typename T, int D, int BM, int BN, int STAGES, typename OutT, int KSPLIT = 1, bool PERSIST = false,
-          bool RAGGED = false, bool CAUSAL = false>
+          bool RAGGED = false, bool CAUSAL = false, bool CHECK = false>
 __global__ void __launch_bounds__(BM / 32 * kWave * KSPLIT)
-__attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, RAGGED, CAUSAL>())))
+__attribute__((amdgpu_waves_per_eu(mfma_min_waves<T, D, PERSIST, RAGGED, CAUSAL, CHECK>())))
 fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
             OutT* __restrict__ O, int N, int num_qblocks, int total_blocks, float scale_log2, int causal,
             int cus_per_xcd, int walk) {
@@ -173,6 +179,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   static_assert(!PERSIST || (KSPLIT == 1 && STAGES == 2), "persistent form: two stages, no key split");
   static_assert(!RAGGED || PERSIST, "RAGGED selects the persistent form whose last key tile is partial");
   static_assert(!CAUSAL || (PERSIST && !RAGGED && BM % (2 * BN) == 0), "CAUSAL selects the persistent causal form");
+  static_assert(!CHECK || (std::is_same<T, f16>::value && STAGES == 2 && KSPLIT == 1 && !CAUSAL),
+                "CHECK: the fp16 two-stage forms without key split, not the causal one");
 
   // One LDS object per stage and matrix: the compiler then sees that a tile load into one stage
   // cannot alias the operand reads from another, and does not make those reads wait for it.
@@ -538,8 +546,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   };
   static_assert(CPT < 16, "prologue wait: vmcnt(CPT) in the low vmcnt bits");
 
-  if constexpr (STAGES == 2 && std::is_same<T, bf16>::value) {
-    // bf16: overflow check instead of a row max. The exponent's reference point is
+  if constexpr (STAGES == 2 && (std::is_same<T, bf16>::value || CHECK)) {
+    // bf16 (and fp16 with CHECK): overflow check instead of a row max. The exponent's reference point is
     // m_ref = m + kShift, so the P.V operand is P' = 2^(S c - m_ref) = P 2^-kShift and
     // "some P > 2^kLazyLog2" is "some rounded P' >= 2": bit 14 of the bf16 pattern (the top
     // exponent bit), tested by one OR over the packed P' registers. bf16 has fp32's exponent
@@ -549,18 +557,47 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     // the fp16 path, done after the exponentials instead of before them. The finite start value
     // of m_ref makes every finite score of a row's first visible tile overflow (a rescale) and
     // keeps a masked score at P' = 0 without a NaN.
-    constexpr float kShift = kLazyLog2 - 1.f;
-    constexpr uint32_t kTopExp = 0x40004000u;   // exponent MSB of both bf16 halves
+    // fp16 (CHECK): fp16 has no room below for the 2^-7 shift (P' would turn subnormal 7 octaves
+    // earlier), and one exponent bit gives no larger window. The check is instead the packed fp16
+    // max of the P' registers (v_pk_maximum3_f16, as many instructions as the OR), compared once
+    // with 2^14; with m_ref = m + 4 that lets a row's max grow 18 octaves past the reference
+    // before a rescale (P' <= 2^14 < fp16's 65504; the P' of keys within 10 octaves of the
+    // reference stay normal). Peaked rows (C5: scores spread ~13 octaves) then rescale about once
+    // instead of at every new maximum. A P' that overflowed fp16 reads as inf in the max and fires.
+    constexpr bool kPackedMax = std::is_same<T, f16>::value;
+    constexpr float kShift = kPackedMax ? 4.f : kLazyLog2 - 1.f;
+    constexpr float kFireF16 = 16384.f;         // fp16: fire when some rounded P' >= 2^14
+    constexpr uint32_t kTopExp = 0x40004000u;   // bf16: exponent MSB of both halves (P' >= 2)
+    // A check word that fires: the bf16 bits, or fp16 (inf, inf) for the packed max.
+    constexpr uint32_t kForce = kPackedMax ? 0x7C007C00u : kTopExp;
     constexpr int HALF = PV_STEPS / 2;
     float m_ref = -3.0e38f;
-    // OR of the P' patterns of one operand register into the check word; the check fires when
-    // some lane of the wave has the top exponent bit set.
+    // The check word of one operand register folded into acc: bf16, the OR of the P' patterns
+    // (the check fires when some lane of the wave has the top exponent bit set); fp16, the packed
+    // max of the P' values (it fires when some lane's max reaches 2^14).
+    typedef _Float16 H2 __attribute__((ext_vector_type(2)));
     auto check_acc = [&](const V8& a, uint32_t acc) __attribute__((always_inline)) -> uint32_t {
-      const u32x4 x = __builtin_bit_cast(u32x4, a);
-      return acc | x[0] | x[1] | x[2] | x[3];
+      if constexpr (kPackedMax) {
+        // (pairs taken with shufflevector: with this compiler, bit-casting single elements of the
+        // u32x4 view of the register read element 0 for every index)
+        H2 mx = __builtin_bit_cast(H2, acc);
+        mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, __builtin_shufflevector(a, a, 0, 1)),
+                                           __builtin_shufflevector(a, a, 2, 3));
+        mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, __builtin_shufflevector(a, a, 4, 5)),
+                                           __builtin_shufflevector(a, a, 6, 7));
+        return __builtin_bit_cast(uint32_t, mx);
+      } else {
+        const u32x4 x = __builtin_bit_cast(u32x4, a);
+        return acc | x[0] | x[1] | x[2] | x[3];
+      }
     };
     auto check_fires = [&](uint32_t acc) __attribute__((always_inline)) -> bool {
-      return __builtin_amdgcn_ballot_w64((acc & kTopExp) != 0) != 0;
+      if constexpr (kPackedMax) {
+        const H2 mx = __builtin_bit_cast(H2, acc);
+        return __builtin_amdgcn_ballot_w64(fmaxf((float)mx[0], (float)mx[1]) >= kFireF16) != 0;
+      } else {
+        return __builtin_amdgcn_ballot_w64((acc & kTopExp) != 0) != 0;
+      }
     };
     // `opaque` hides -m_ref behind an empty asm so that the fast path's exponentials are not
     // merged with the generic path's and hoisted out of the MFMA phases.
@@ -599,7 +636,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
     // tile's exact max).
     f32x16 sa[NKB], sb[NKB];
     V8 pa[PV_STEPS], pb[PV_STEPS];
-    uint32_t or_c = kTopExp;
+    uint32_t or_c = kForce;
     // S(0) and the first half of P'(0) of a block (the arrays are parameters, not captures:
     // capturing them here changes how the compiler allocates the whole kernel).
     auto first_tile = [&](f32x16 (&s0)[NKB], V8 (&p0)[PV_STEPS]) {
@@ -774,7 +811,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
             qk(sn, kn);
             if constexpr (!PERSIST || RAGGED) mask(sn, opaque_offset(tile_of(t + 1) * BN));
           }
-          or_c = kTopExp;   // no P'(t+1) half was made: a fast iteration after this one recomputes
+          or_c = kForce;   // no P'(t+1) half was made: a fast iteration after this one recomputes
         }
       }
       __builtin_amdgcn_s_waitcnt(0);

@@ -126,14 +126,15 @@ int persistent_grid(long long total_blocks, int wgs_per_cu) {
 
 // Workgroups of an fa_mfma_fwd instantiation that fit on one CU of the current device (queried
 // once per device), 0 if unknown.
-template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool PERSIST, bool RAGGED, bool CAUSAL>
+template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS, bool PERSIST, bool RAGGED, bool CAUSAL,
+          bool CHECK = false>
 int wgs_per_cu() {
   static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, PERSIST, RAGGED, CAUSAL>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, PERSIST, RAGGED, CAUSAL, CHECK>,
                                                      BM / 32 * pa::kWave * KS, 0) != hipSuccess || n <= 0)
       return 0;
     cache[dev].store(n, std::memory_order_relaxed);
@@ -175,18 +176,31 @@ PersistentPlan persistent_grid_for(int64_t n, int64_t bh, int causal) {
     if (grid <= 0) return {};
     return {grid, pa::causal_walk(n, bh, BM, BN, grid / pa::kNumXcd, cus, D == 64, per_xcd)};
   }
-  const int clean = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, false>();
+  constexpr bool kCheck = std::is_same<T, pa::f16>::value;   // the fp16 non-causal forms' packed-max check
+  const int clean = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, false, false, kCheck>();
   if (n % (2 * BN) == 0) return {persistent_grid(total, clean), 0};
-  const int ragged = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, true, false>();
+  const int ragged = wgs_per_cu<T, D, BM, BN, ST, OutT, KS, true, true, false, kCheck>();
   return ragged >= clean ? PersistentPlan{persistent_grid(total, ragged), 0} : PersistentPlan{};
 }
 
+// fused_tc with fp16 inputs on non-causal rows (two stages, no key split) uses the packed-max
+// check instead of the per-tile row max (kernel template argument CHECK) in its persistent forms,
+// and at d = 128 also in the per-block form (so both launch forms of a d = 128 call give the same
+// bits); causal rows, the d = 64 per-block form, the key split and the fused_tuned tiles keep the
+// row max. Measured back to back, row max -> packed-max check (TFLOP/s), persistent: d = 64
+// 8x16x1024 (C3) 777 -> 806 and 694 -> 728, 1x16x8192 with Q, K x3 (C5) 926 -> 944 and 945 -> 966,
+// 4x16x4096 888 -> 927, 16x16x2048 863 -> 899, 4x16x4032 (ragged) 863 -> 898, 8x16x1000 (ragged)
+// 748 -> 744; d = 128 4x32x4096 1080 -> 1152. Per block: d = 128 4x32x4096 1048 -> 1100, 1x32x1030
+// 487 -> 524; d = 64 it lost (2 waves per SIMD, 194 VGPRs: C3 716 -> 696, 8x16x1025 602 -> 554;
+// held to 3 with 16 VGPRs spilled: 437), and on causal d = 64 rows 9 % at 8x16x1024.
 template <typename T, int D, int BM, int BN, int ST, typename OutT, int KS = 1, bool TC = false>
 hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int bh, int n, int causal,
                        hipStream_t stream) {
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;
   if (total > INT_MAX) return hipErrorInvalidConfiguration;
+  constexpr bool kCheck = TC && ST == 2 && KS == 1 && std::is_same<T, pa::f16>::value;
+  constexpr bool kCheckPerBlock = kCheck && D == 128;
   if constexpr (TC && ST == 2 && KS == 1) {
     {
       const PersistentPlan plan = persistent_grid_for<T, D, BM, BN, ST, OutT, KS>(n, bh, causal);
@@ -195,8 +209,8 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
         // even tile count whose last tile is partial, or an odd count of full tiles, padded with
         // an empty one) the RAGGED form, whose wrap copies mask the keys past N.
         auto kernel = causal ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false, true>
-                      : n % (2 * BN) == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false>
-                                          : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true>;
+                      : n % (2 * BN) == 0 ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, false, false, kCheck>
+                                          : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, true, true, false, kCheck>;
         hipLaunchKernelGGL(kernel, dim3((unsigned)plan.grid), dim3(BM / 32 * pa::kWave * KS), 0, stream,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                            static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal,
@@ -205,8 +219,10 @@ hipError_t launch_mfma(const void* q, const void* k, const void* v, void* o, int
       }
     }
   }
-  hipLaunchKernelGGL((pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS>), dim3((unsigned)total), dim3(BM / 32 * pa::kWave * KS), 0,
-                     stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+  auto kernel = kCheckPerBlock && !causal ? pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS, false, false, false, kCheckPerBlock>
+                                          : pa::fa_mfma_fwd<T, D, BM, BN, ST, OutT, KS>;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(BM / 32 * pa::kWave * KS), 0, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<OutT*>(o), n, qblocks, (int)total, scale_log2_for(D), causal, 0, 0);
   return hipGetLastError();
 }
@@ -542,12 +558,13 @@ const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, 
   const long long total = (n + e->br - 1) / e->br * bh;
   const PersistentPlan plan = e->persistent_grid ? e->persistent_grid(n, bh, causal) : PersistentPlan{};
   const bool pers = plan.grid > 0;   // as in launch_mfma: no device (grid 0) means one workgroup per block
-  snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s> grid %d x %d threads",
+  const bool check = e->dtype == PA_DTYPE_F16 && e->tc && e->db && e->ks == 1 && !causal && (pers || e->d == 128);   // as in launch_mfma
+  snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s%s%s> grid %d x %d threads",
            dt_name[e->dtype], e->d, e->br, e->bc, e->db ? 2 : 1, dt_name[e->out_dtype],
            e->ks == 2 ? ", key split 2" : "", pers ? ", persistent" : "",
            !pers ? "" : !causal ? (n % (2 * e->bc) ? ", ragged" : "")
                       : plan.walk == 2 ? ", causal, device list" : plan.walk == 1 ? ", causal, by rank" : ", causal",
-           pers ? plan.grid : (int)total, e->br / 32 * pa::kWave * e->ks);
+           check ? ", packed-max check" : "", pers ? plan.grid : (int)total, e->br / 32 * pa::kWave * e->ks);
   return desc;
 }
 

@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <type_traits>
 
 #include "phantom_attn.h"
 #include "phantom_attn_tiles.h"
@@ -46,7 +47,10 @@ struct Candidate {
 template <typename T, int D, int BM, int BN, int ST, bool PERSIST>
 hipError_t launch(const void* q, const void* k, const void* v, void* o, int bh, int n, hipStream_t stream,
                   int* grid_out, bool dry) {
-  auto kernel = pa::fa_mfma_fwd<T, D, BM, BN, ST, T, 1, PERSIST, false, false>;
+  // fp16 two-stage candidates take the packed-max check, as fused_tc's fp16 tiles do on these
+  // (non-causal) calls, so that they compare like with like.
+  constexpr bool kCheck = std::is_same<T, pa::f16>::value && ST == 2;
+  auto kernel = pa::fa_mfma_fwd<T, D, BM, BN, ST, T, 1, PERSIST, false, false, kCheck>;
   const int threads = BM / 32 * pa::kWave;
   const int qblocks = (n + BM - 1) / BM;
   const long long total = (long long)qblocks * bh;

@@ -20,13 +20,13 @@ REPO = os.path.abspath(os.path.join(HERE, "..", "..", ".."))
 PKG = os.path.join(REPO, "phantom-a100_amd")
 # Kernels kept, by the mangled name up to the end of the template arguments (the parameter list
 # that follows is not matched, so a change of the kernel's signature keeps the fixture regenerable):
-# the naive softmax, a per-block fused_tc d=64 kernel (fp16 in, fp32 out), the persistent C4
+# the naive softmax, the persistent fused_tc d=64 kernel (fp16 in, fp32 out, packed-max check), the persistent C4
 # kernel (bf16 d=128, BM=256), a one-stage fused_tuned tile and the fp32 fused kernel.
 KERNELS = [
     "_ZN2pa13naive_softmaxE",
-    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi64ELi2EfLi1ELb0ELb0ELb0EEEv",
-    "_ZN2pa11fa_mfma_fwdIDF16bLi128ELi256ELi64ELi2EDF16bLi1ELb1ELb0ELb0EEEv",
-    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi32ELi1EDF16_Li1ELb0ELb0ELb0EEEv",
+    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi64ELi2EfLi1ELb1ELb0ELb0ELb1EEEv",
+    "_ZN2pa11fa_mfma_fwdIDF16bLi128ELi256ELi64ELi2EDF16bLi1ELb1ELb0ELb0ELb0EEEv",
+    "_ZN2pa11fa_mfma_fwdIDF16_Li64ELi128ELi32ELi1EDF16_Li1ELb0ELb0ELb0ELb0EEEv",
     "_ZN2pa10fa_f32_fwdIfLi64ELi4EfEEv",
 ]
 

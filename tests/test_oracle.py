@@ -394,6 +394,88 @@ def test_kernel_model_two_term_p_on_single_tile_rows(n, causal):
         assert np.abs(one[:, single] - ref[:, single]).max() > 4 * np.abs(two[:, single] - ref[:, single]).max()
 
 
+# ---------------------------------------------------------------- 9. the fp16 kernels' packed-max check
+F16_CHECK = dict(check="rounded", shift=4.0, fire=2.0 ** 14)   # fp16 non-causal persistent forms
+
+
+def test_f16_packed_max_order_is_the_value_order():
+    """Every non-negative fp16 value up to +inf: the packed max (v_pk_maximum3_f16) of the P'
+    registers reaches 2^14 exactly when some P' does, and a P' that overflowed to inf reads as
+    >= 2^14 too (it fires and is recomputed)."""
+    pats = np.arange(0, 0x7C01, dtype=np.uint16)              # +0 .. +inf
+    vals = pats.view(np.float16).astype(np.float32)
+    rng = np.random.default_rng(28)
+    for _ in range(200):
+        pick = rng.choice(vals, 8)
+        assert (np.maximum.reduce(pick) >= 2.0 ** 14) == np.any(pick >= 2.0 ** 14)
+    assert np.float32(np.float16(np.inf)) >= 2.0 ** 14
+    with np.errstate(over="ignore"):
+        assert np.float16(np.float32(65520.0)) == np.inf      # the first fp32 value fp16 rounds to inf
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [1.0, 4.0])
+def test_kernel_model_f16_check_is_exact(causal, scale):
+    """The fp16 rule (m_ref = m + 4, fire when some P' >= 2^14) with unrounded P: O / l equals
+    float64 softmax to float32 accuracy, P = P' 2^4 stays below 2^18, and it rescales no more
+    often than the row-max rule with its 2^8 window."""
+    rng = np.random.default_rng(29)
+    q, k, v = (rng.standard_normal((1, 2, 300, 64)).astype(np.float32) for _ in range(3))
+    q *= scale
+    st_r, st_m = {}, {}
+    got = oracle.attention_kernel_model(q, k, v, causal, stats=st_r, **F16_CHECK)
+    oracle.attention_kernel_model(q, k, v, causal, lazy_log2=8.0, stats=st_m, check="max")
+    assert np.abs(got - attention_naive(q, k, v, causal)).max() < 2e-5
+    assert st_r["p_max"] < 2.0 ** 18
+    assert st_r["rescales"] <= st_m["rescales"]
+
+
+def test_kernel_model_f16_check_on_growing_and_peaked_rows():
+    """Rows whose max keeps growing (18 octaves over the row) rescale under the fp16 rule and still
+    match float64; peaked rows (scores spread ~13 octaves, as in C5) rescale less often than with
+    the row-max rule, within the fp16 bar."""
+    n, d = 512, 16
+    q = np.ones((1, 1, n, d), np.float32)
+    k = (np.linspace(0, 50, n, dtype=np.float32)[:, None] * np.ones((1, d), np.float32))[None, None]
+    v = np.random.default_rng(30).standard_normal((1, 1, n, d)).astype(np.float32)
+    st = {}
+    got = oracle.attention_kernel_model(q, k, v, stats=st, p_dtype="float16", **F16_CHECK)
+    assert st["rescales"] >= 1 and st["p_max"] < 2.0 ** 18
+    assert np.abs(got - attention_naive(q, k, v)).max() < 2e-3
+    rng = np.random.default_rng(31)
+    qp, kp, vp = (rng.standard_normal((1, 4, 1024, 64)).astype(np.float32) for _ in range(3))
+    qp, kp = (oracle.round_to(3 * x, "float16") for x in (qp, kp))
+    vp = oracle.round_to(vp, "float16")
+    st_r, st_m = {}, {}
+    got = oracle.attention_kernel_model(qp, kp, vp, stats=st_r, p_dtype="float16", **F16_CHECK)
+    oracle.attention_kernel_model(qp, kp, vp, lazy_log2=8.0, stats=st_m, p_dtype="float16", check="max")
+    assert st_r["rescales"] < st_m["rescales"]
+    assert np.abs(got - attention_naive(qp, kp, vp)).max() < 2e-3
+
+
+def test_kernel_model_f16_check_dominant_key_returns_its_value():
+    """A dominant key whose P' = 2^(x - m_ref) is not an fp16 value: l sums the rounded P', so the
+    key's V comes back exactly, as under the other rules."""
+    n, d = 64, 64
+    rng = np.random.default_rng(32)
+    v = rng.standard_normal((1, 1, n, d)).astype(np.float32)
+    s_log2 = np.full((n, n), -200.0, np.float32)
+    s_log2[:, 0] = 0.0
+    s_log2[:, 40] = 11.3                      # past the row-max rule's 2^8 window, inside 2^(14+4)
+    scale_log2 = np.float32(oracle.LOG2E / np.sqrt(d))
+    q = np.eye(n, d, dtype=np.float32)[None, None]
+    k = np.zeros((1, 1, n, d), np.float32)
+    k[0, 0, :, :n] = (s_log2 / scale_log2).T
+    st = {}
+    got = oracle.attention_kernel_model(q, k, v, p_dtype="float16", bc=32, stats=st, **F16_CHECK)
+    assert st["rescales"] == 0                # 11.3 - 4 octaves above m_ref: P' < 2^14, no rescale
+    p40 = np.float32(2.0) ** np.float32(11.3 - 4.0)
+    w40 = oracle.round_to(np.array([p40], np.float32), "float16")[0]
+    w0 = np.float32(2.0 ** -4)
+    want = (w40 * v[0, 0, 40] + w0 * v[0, 0, 0]) / (w40 + w0)
+    np.testing.assert_allclose(got[0, 0], np.broadcast_to(want, (n, d)), rtol=2e-6, atol=2e-6)
+
+
 def test_kernel_model_rejects_unknown_check():
     with pytest.raises(ValueError):
         oracle.attention_kernel_model(np.zeros((1, 4, 8), np.float32), np.zeros((1, 4, 8), np.float32),
