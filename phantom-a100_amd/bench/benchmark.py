@@ -5,7 +5,8 @@
 
 Same harness behaviour and CSV schema as the reference's bench/benchmark.py:106-190:
   * every run is first checked against the fp32 SDPA reference (``cuda_attn.reference``); a
-    result outside the gate is written as ``wrong_result`` and never timed;
+    result outside the gate (1e-4 fp32, 2e-3 fp16; bf16: ``gate_bar``) is written as
+    ``wrong_result`` and never timed;
   * timing: warm-up calls, then per timed call a zeroing of a flush buffer followed by one call
     between two HIP events; median and 10th / 90th percentiles;
   * peak device memory of one call above what was live before it (caching-allocator statistics);
@@ -67,27 +68,58 @@ ACCEPTS = {"fused_vec": (torch.float16,), "fused_db": (torch.float16,),
            "fused": (torch.float16, torch.float32)}
 
 
-def gate_tolerance(dtype: torch.dtype, causal: bool = False, vmax: float = 0.0) -> float:
-    """The reference's pass bar (/root/reference/bench/benchmark.py:170): 2e-3 for 16-bit inputs.
-    bf16 (an extension) with a causal mask: the first rows average over a handful of keys, so one
-    weight rounded to bf16 (8-bit significand) moves O by up to half a bf16 ulp of max|V|; the bar
-    is then max(2e-3, 1.25 * 2^-9 * max|V|), the bound the GPU parity tests use. torch's own SDPA
-    in bf16 needs the same allowance."""
+BF16_U = 2.0 ** -8   # bf16 unit roundoff: rounding to nearest moves x by at most 2^-8 |x|
+
+
+def half_ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    """Half the spacing of bf16 values at |x| (8 significant bits): for |x| in [2^(e-1), 2^e) the
+    spacing is 2^(e-8), so rounding x to bf16 moves it by at most 2^(e-9)."""
+    _, e = torch.frexp(x.float())
+    return torch.ldexp(torch.ones_like(x, dtype=torch.float32), e - 9)
+
+
+def gate_bar(dtype: torch.dtype, ref: torch.Tensor, ref_absv: torch.Tensor | None = None,
+             out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Element-wise pass bar of an output against the fp32 reference `ref`.
+
+    fp32 inputs: 1e-4; fp16 inputs: 2e-3, the reference's bars (/root/reference/bench/benchmark.py:170).
+    bf16 inputs (an extension): the attention weights P are rounded to bf16 before P.V, and one
+    rounding can move an output further than 2e-3 on rows of few keys. With every weight rounded,
+    p~ = p (1 + e), |e| <= u = 2^-8, and l the sum of the weights (rounded or not), the output moves by
+    at most u / (1 - u) * (sum_j p_j |V_j| / sum_j p_j + |O|) (O~ - O = sum_j (p~_j - p_j) (V_j - O) / l~,
+    since sum_j p_j (V_j - O) = 0). `ref_absv` is the first term, the reference attention of |V|.
+    The bar is the larger of 2e-3 and that bound, element by element: it widens only where the
+    weights' rounding can reach past 2e-3. A bf16 output also carries its own rounding: half a bf16
+    ulp of the output is added."""
     if dtype == torch.float32:
-        return 1e-4
-    if dtype == torch.bfloat16 and causal:
-        return max(2e-3, 1.25 * 2.0 ** -9 * vmax)
-    return 2e-3
+        return torch.full_like(ref, 1e-4)
+    bar = torch.full_like(ref, 2e-3)
+    if dtype == torch.bfloat16:
+        if ref_absv is None:
+            raise ValueError("bf16 gate: the reference attention of |V| is needed")
+        bar = torch.maximum(bar, BF16_U / (1 - BF16_U) * (ref_absv + ref.abs()))
+    if out_dtype == torch.bfloat16:
+        bar = bar + half_ulp_bf16(ref)
+    return bar
 
 
-def gate_error(out: torch.Tensor, ref: torch.Tensor) -> float:
-    """Max abs error against the fp32 reference. A bf16 output (an extension: the reference's
-    kernels return fp16) is also allowed its own rounding, half a bf16 ulp = 2^-9 |ref|, which
-    alone exceeds 2e-3 wherever |O| > 1 (short causal rows)."""
+def gate(out: torch.Tensor, ref: torch.Tensor, bar: torch.Tensor) -> tuple[float, bool]:
+    """(max abs error against the fp32 reference, every element within its bar)."""
     err = (out.float() - ref).abs()
-    if out.dtype == torch.bfloat16:
-        err = err - ref.abs() * 2.0 ** -9
-    return err.max().item()
+    return err.max().item(), bool((err <= bar).all().item())
+
+
+def reference_pair(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool):
+    """What the gate compares with: the fp32 SDPA reference and, for bf16 inputs, the fp32
+    reference attention of |V| (gate_bar's bound), else None."""
+    return (cuda_attn.reference(q, k, v, causal),
+            cuda_attn.reference(q, k, v.abs(), causal) if q.dtype == torch.bfloat16 else None)
+
+
+def gate_against(out: torch.Tensor, ref_pair, in_dtype: torch.dtype) -> tuple[float, bool]:
+    """gate() of one output against reference_pair() of its inputs."""
+    ref32, ref_absv = ref_pair
+    return gate(out, ref32, gate_bar(in_dtype, ref32, ref_absv, out.dtype))
 
 
 def workspace_bytes(name: str, b: int, h: int, n: int, d: int, elem: int) -> int:
@@ -185,7 +217,8 @@ class Sweep:
 
     def measure(self, name: str, q, k, v, causal: bool, ref) -> dict:
         """The CSV row of one implementation at one shape: a status row if it cannot run here, else
-        gated against the fp32 reference, then timed and its allocation peak taken."""
+        gated against `ref` (reference_pair() of the inputs, None above --ref-max-n), then timed
+        and its allocation peak taken."""
         b, h, n, d = q.shape
         row = dict(self.meta, impl=name, dtype=self.args.dtype, causal=causal, B=b, H=h, N=n, d=d)
         status = status_before_run(name, q.dtype, d)
@@ -200,10 +233,12 @@ class Sweep:
             return impl(q, k, v, causal)
 
         try:
-            err = gate_error(call(), ref) if ref is not None else float("nan")
-            if err > gate_tolerance(q.dtype, causal, v.abs().max().item()):
-                row.update(max_abs_err=f"{err:.2e}", status="wrong_result")
-                return row
+            err = float("nan")
+            if ref is not None:
+                err, ok = gate_against(call(), ref, q.dtype)
+                if not ok:
+                    row.update(max_abs_err=f"{err:.2e}", status="wrong_result")
+                    return row
             # naive re-reads S from HBM three times per call: fewer timed calls past N = 2048
             iters = self.args.iters if name != "naive" or n <= 2048 else max(10, self.args.iters // 10)
             med, p10, p90 = time_calls(call, self.args.warmup, iters, self.flush)
@@ -228,7 +263,7 @@ class Sweep:
             writer.writeheader()
             for causal, n in self.shapes():
                 q, k, v = self.inputs(n)
-                ref = cuda_attn.reference(q, k, v, causal) if n <= self.args.ref_max_n else None
+                ref = reference_pair(q, k, v, causal) if n <= self.args.ref_max_n else None
                 for name in self.args.impls:
                     row = self.measure(name, q, k, v, causal, ref)
                     writer.writerow(row)

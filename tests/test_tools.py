@@ -77,29 +77,105 @@ def test_summary_statistics():
     assert benchmark.summarize([2.0]) == (2.0, 2.0, 2.0)
 
 
-def test_bf16_gate_allows_only_the_outputs_rounding():
+def test_bf16_half_ulp_is_the_largest_rounding_move():
+    """Over every finite positive bf16 pattern's midpoints to its neighbours: rounding to bf16 moves a
+    value by at most half_ulp_bf16, and a value just past the midpoint moves by almost exactly that."""
+    pats = torch.arange(0x0080, 0x7F7F, dtype=torch.int32).to(torch.int16)   # normal bf16, +0x80 .. max-1
+    lo = pats.view(torch.bfloat16).float()
+    hi = (pats + 1).view(torch.bfloat16).float()
+    mid = (lo.double() + hi.double()) / 2
+    x = torch.nextafter(mid, torch.zeros_like(mid)).float()                    # just below the midpoint
+    moved = (x.to(torch.bfloat16).float().double() - x.double()).abs()
+    bound = benchmark.half_ulp_bf16(x).double()
+    assert (moved <= bound).all()
+    assert ((bound - moved) <= bound * 2.0 ** -14).all()
+    assert benchmark.half_ulp_bf16(torch.tensor([1.0, 1.99, 2.0, 0.75])).tolist() == [2.0 ** -8, 2.0 ** -8,
+                                                                                       2.0 ** -7, 2.0 ** -9]
+
+
+def test_gate_bars_for_fp32_and_fp16_are_the_references():
     ref = torch.tensor([3.0, -2.5, 0.1])
+    assert (benchmark.gate_bar(torch.float32, ref) == 1e-4).all()
+    assert (benchmark.gate_bar(torch.float16, ref, out_dtype=torch.float16) == 2e-3).all()
+    out16 = ref.to(torch.float16)
+    err, ok = benchmark.gate(out16, ref, benchmark.gate_bar(torch.float16, ref, out_dtype=torch.float16))
+    assert ok and err == (out16.float() - ref).abs().max().item()
+    err, ok = benchmark.gate(ref + 3e-3, ref, benchmark.gate_bar(torch.float16, ref))
+    assert not ok and err == pytest.approx(3e-3, rel=1e-4)
+
+
+def _bf16_weights_attention(s, v):
+    """O with every weight rounded to bf16 and l the sum of the rounded weights (float64)."""
+    p = torch.softmax(s.double(), dim=-1)
+    pr = p.float().to(torch.bfloat16).double()
+    return (pr @ v.double()) / pr.sum(-1, keepdim=True), p @ v.double(), p @ v.double().abs()
+
+
+def test_bf16_gate_admits_the_weights_rounding_and_no_more():
+    """Two keys with weights near 0.4 / 0.6 and V = +4 / -4: rounding the weights to bf16 moves O
+    past 2e-3, inside the bound u / (1 - u) (sum p|V| + |O|); a planted error of twice the bound
+    fails, and so does one of 3e-3 on a row whose bound stays under 2e-3."""
+    s = torch.tensor([[0.0, 0.41]])                   # p = 0.398.. / 0.601..
+    v = torch.tensor([[4.0], [-4.0]])
+    got, ref, ref_absv = _bf16_weights_attention(s, v)
+    ref, ref_absv, got = ref.float(), ref_absv.float(), got.float()
+    moved = (got - ref).abs().item()
+    assert moved > 2e-3
+    bar = benchmark.gate_bar(torch.bfloat16, ref, ref_absv, out_dtype=torch.float32)
+    assert moved <= bar.item()
+    assert benchmark.gate(got, ref, bar)[1]
+    assert not benchmark.gate(ref + 2 * bar, ref, bar)[1]
+    # many keys of similar weight and small |V|: the bound is below 2e-3, the bar stays there
+    g = torch.Generator().manual_seed(5)
+    s = torch.randn(4, 512, generator=g) * 0.1
+    v = torch.randn(512, 8, generator=g) * 0.2
+    got, ref, ref_absv = (t.float() for t in _bf16_weights_attention(s, v))
+    bar = benchmark.gate_bar(torch.bfloat16, ref, ref_absv, out_dtype=torch.float32)
+    assert (bar == 2e-3).all() and benchmark.gate(got, ref, bar)[1]
+    assert not benchmark.gate(ref + 3e-3, ref, bar)[1]
+
+
+def test_bf16_gate_bound_holds_on_random_rows():
+    """The bound is a worst case: over random rows of 1-64 keys (the short causal rows where it
+    matters), rounding every weight to bf16 never moves O past it."""
+    g = torch.Generator().manual_seed(6)
+    for keys in (1, 2, 3, 5, 8, 17, 64):
+        s = torch.randn(256, keys, generator=g) * 3
+        v = torch.randn(keys, 16, generator=g) * 2
+        got, ref, ref_absv = _bf16_weights_attention(s, v)
+        bound = benchmark.BF16_U / (1 - benchmark.BF16_U) * (ref_absv + ref.abs())
+        assert ((got - ref).abs() <= bound * (1 + 1e-9)).all(), keys
+
+
+def test_gate_against_reference_pair_on_attention():
+    """The harness's own path: reference_pair() of bf16 inputs (fp32 SDPA, on the CPU here) and
+    gate_against() of an output whose weights were rounded to bf16 pass, causal rows included;
+    the same output shifted by 0.05 on one row fails. fp16 inputs need no |V| reference."""
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(1, 2, 96, 32, generator=g).to(torch.bfloat16) for _ in range(3))
+    for causal in (False, True):
+        pair = benchmark.reference_pair(q, k, v, causal)
+        assert pair[1] is not None and pair[1].shape == pair[0].shape
+        s = (q.double() @ k.double().transpose(-1, -2)) / 32 ** 0.5
+        if causal:
+            s = s.masked_fill(torch.ones(96, 96, dtype=torch.bool).triu(1), float("-inf"))
+        p = torch.softmax(s, -1).float().to(torch.bfloat16).double()
+        out = ((p @ v.double()) / p.sum(-1, keepdim=True)).to(torch.bfloat16)
+        err, ok = benchmark.gate_against(out, pair, torch.bfloat16)
+        assert ok, err
+        bad = out.clone()
+        bad[0, 1, 40] += 0.05
+        assert not benchmark.gate_against(bad, pair, torch.bfloat16)[1]
+    assert benchmark.reference_pair(q.half(), k.half(), v.half(), False)[1] is None
+
+
+def test_bf16_gate_allows_the_outputs_rounding():
+    ref = torch.tensor([3.0, -2.5, 0.1, 1.0 + 2.0 ** -8 + 2.0 ** -12])
+    absv = ref.abs()
     out = ref.to(torch.bfloat16)                      # pure output rounding: passes
-    assert benchmark.gate_error(out, ref) <= benchmark.gate_tolerance(torch.bfloat16)
-    bad = (ref + torch.tensor([0.0, 0.0, 0.01])).to(torch.bfloat16)
-    assert benchmark.gate_error(bad, ref) > benchmark.gate_tolerance(torch.bfloat16)
-    out16 = ref.to(torch.float16)                     # fp16 keeps the reference's plain bar
-    assert benchmark.gate_error(out16, ref) == (out16.float() - ref).abs().max().item()
-
-
-def test_bf16_causal_gate_allows_one_rounded_weight():
-    """bf16 with a causal mask: the first row's single key carries all the weight; one weight
-    rounded to bf16 moves O by half a bf16 ulp of max|V|, which the causal bf16 bar admits."""
-    assert benchmark.gate_tolerance(torch.bfloat16, causal=False, vmax=4.0) == 2e-3
-    assert benchmark.gate_tolerance(torch.bfloat16, causal=True, vmax=0.5) == 2e-3
-    tol = benchmark.gate_tolerance(torch.bfloat16, causal=True, vmax=4.0)
-    assert tol == pytest.approx(1.25 * 2.0 ** -9 * 4.0)
-    # two keys, weights 0.4 / 0.6 with V = +4 / -4: rounding the weight 0.4 to bf16 moves O by
-    # 4 * 2 * |0.4 - bf16(0.4)| (both weights shift, V differs by 8), inside the bar
-    w = torch.tensor(0.4)
-    shift = 4.0 * 2 * (w - w.to(torch.bfloat16).float()).abs().item()
-    assert 2e-3 < shift <= tol
-    assert benchmark.gate_tolerance(torch.float16, causal=True, vmax=4.0) == 2e-3
+    bar = benchmark.gate_bar(torch.bfloat16, ref, absv, out_dtype=torch.bfloat16)
+    assert benchmark.gate(out, ref, bar)[1]
+    assert not benchmark.gate((ref + torch.tensor([0.0, 0.0, 0.01, 0.0])).to(torch.bfloat16), ref, bar)[1]
 
 
 def test_tile_sweep_points_and_rows():
