@@ -27,8 +27,10 @@ const char* pa_tiles_label(int index);
 
 /* The candidate's input dtype, head dim, query rows per workgroup (br), keys per tile (bc), LDS
  * stages and launch form (persistent 1: as many workgroups as fit at once walk the query blocks;
- * 0: one workgroup per query block). */
-int pa_tiles_describe(int index, int* dtype, int* d, int* br, int* bc, int* stages, int* persistent);
+ * 0: one workgroup per query block), and for a persistent candidate the most workgroups it
+ * places per CU (0: as many as fit). */
+int pa_tiles_describe(int index, int* dtype, int* d, int* br, int* bc, int* stages, int* persistent,
+                      int* wgs_per_cu);
 
 /* O = softmax(Q K^T / sqrt(d)) V with candidate `index`, as pa_fused_tc_fwd (output in the input
  * dtype). Only non-causal calls of the candidate's dtype and head dim; the persistent candidates

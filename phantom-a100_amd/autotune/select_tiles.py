@@ -99,9 +99,9 @@ def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal:
         finally:
             _native.set_persistent(prev)
     grid = re.search(r"grid (\d+) x", desc)
-    # fp16 two-stage fused_tc tiles on non-causal rows use the packed-max check in the persistent
-    # forms and at d = 128 per block (the launcher names it); the fp16 two-stage alternatives always
-    check = ", packed-max check" in desc or (isinstance(source, int) and dtype == torch.float16 and "2 stages" in desc)
+    # fp16 two-stage tiles on non-causal rows use the packed-max check in fused_tc's persistent
+    # forms, at d = 128 per block, and in every alternative; both launchers name it
+    check = ", packed-max check" in desc
     return {"ksplit": 2 if "key split 2" in desc else 1, "persistent": ", persistent" in desc,
             "ragged": ", ragged" in desc, "causal": ", persistent, causal" in desc, "check": check,
             "workgroups": int(grid.group(1)) if grid else -(-n // br) * bh, "description": desc}

@@ -24,7 +24,7 @@ _ip = ctypes.POINTER(ctypes.c_int)
 PROTOTYPES = {
     "pa_tiles_count": (_i, []),
     "pa_tiles_label": (ctypes.c_char_p, [_i]),
-    "pa_tiles_describe": (_i, [_i, _ip, _ip, _ip, _ip, _ip, _ip]),
+    "pa_tiles_describe": (_i, [_i, _ip, _ip, _ip, _ip, _ip, _ip, _ip]),
     "pa_tiles_fwd": (_i, [_i, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i, _p]),
     "pa_tiles_kernel": (ctypes.c_char_p, [_i, _i64, _i64]),
     "pa_tiles_last_error": (ctypes.c_char_p, []),
@@ -57,17 +57,18 @@ def lib() -> ctypes.CDLL:
 
 
 def candidates() -> list[dict]:
-    """Every compiled alternative: index, label, dtype, d, br, bc, stages, persistent."""
+    """Every compiled alternative: index, label, dtype, d, br, bc, stages, persistent, wgs_per_cu
+    (the most workgroups per CU of a persistent launch, 0 for as many as fit)."""
     out = []
     h = lib()
     for i in range(h.pa_tiles_count()):
-        vals = [ctypes.c_int(0) for _ in range(6)]
+        vals = [ctypes.c_int(0) for _ in range(7)]
         rc = h.pa_tiles_describe(i, *(ctypes.byref(x) for x in vals))
         if rc != _native.OK:
             raise RuntimeError(h.pa_tiles_last_error().decode())
-        dt, d, br, bc, st, pers = (x.value for x in vals)
+        dt, d, br, bc, st, pers, cap = (x.value for x in vals)
         out.append({"index": i, "label": h.pa_tiles_label(i).decode(), "dtype": CODE_DTYPE.get(dt), "d": d,
-                    "br": br, "bc": bc, "stages": st, "persistent": bool(pers)})
+                    "br": br, "bc": bc, "stages": st, "persistent": bool(pers), "wgs_per_cu": cap})
     return out
 
 

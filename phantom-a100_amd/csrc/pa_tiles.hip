@@ -3,7 +3,8 @@
 // else. fused_tc launches one tile per head dim; this library launches the shapes that choice was
 // made against, so that each can be timed and profiled with rocprofv3 on the same inputs:
 //   d = 128: 128-query workgroups (two per CU), 32- and 128-key tiles, one LDS stage;
-//   d = 64:  256-query workgroups, 64-query workgroups, 32-key tiles, 128-key tiles.
+//   d = 64:  256-query workgroups, 64-query workgroups, 32-key tiles, 128-key tiles, and the
+//            shipped tile's persistent launch held to two workgroups per CU.
 // The shipped tiles themselves are measured through libphantom_attn.so (both its launch forms).
 // Declarations: include/phantom_attn_tiles.h. Non-causal calls only; same argument checks and
 // status convention as libphantom_attn.so.
@@ -36,15 +37,15 @@ int fail(int code, const char* fmt, ...) {
 typedef hipError_t (*launch_fn)(const void*, const void*, const void*, void*, int, int, hipStream_t, int*, bool);
 
 // One candidate: the kernel's template arguments and whether it takes the persistent launch (as
-// many workgroups as fit at once, walking the query blocks of their XCD; needs N a multiple of
-// 2 * BN, as the shipped persistent form without its ragged copy).
+// many workgroups as fit at once, or at most wgs_cap per CU, walking the query blocks of their
+// XCD; needs N a multiple of 2 * BN, as the shipped persistent form without its ragged copy).
 struct Candidate {
   const char* label;
-  int dtype, d, br, bc, stages, persistent;
+  int dtype, d, br, bc, stages, persistent, wgs_cap;
   launch_fn fn;
 };
 
-template <typename T, int D, int BM, int BN, int ST, bool PERSIST>
+template <typename T, int D, int BM, int BN, int ST, bool PERSIST, int CAP>
 hipError_t launch(const void* q, const void* k, const void* v, void* o, int bh, int n, hipStream_t stream,
                   int* grid_out, bool dry) {
   // fp16 two-stage candidates take the packed-max check, as fused_tc's fp16 tiles do on these
@@ -63,6 +64,7 @@ hipError_t launch(const void* q, const void* k, const void* v, void* o, int bh, 
     if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0);
     if (e != hipSuccess) return e;
     if (per_cu <= 0) return hipErrorInvalidConfiguration;
+    if (CAP > 0) per_cu = std::min(per_cu, CAP);
     cus_per_xcd = cus / pa::kNumXcd;
     const long long per_xcd = (total + pa::kNumXcd - 1) / pa::kNumXcd;
     grid = (int)std::min<long long>((long long)cus_per_xcd * per_cu, per_xcd) * pa::kNumXcd;
@@ -75,19 +77,20 @@ hipError_t launch(const void* q, const void* k, const void* v, void* o, int bh, 
   return hipGetLastError();
 }
 
-#define PA_CAND(label, T, code, D, BM, BN, ST, P) \
-  Candidate { label, code, D, BM, BN, ST, P, &launch<T, D, BM, BN, ST, P> }
+#define PA_CAND(label, T, code, D, BM, BN, ST, P, CAP) \
+  Candidate { label, code, D, BM, BN, ST, P, CAP, &launch<T, D, BM, BN, ST, P, CAP> }
 
 const Candidate kCandidates[] = {
-    PA_CAND("br128_bc64_2stage_persistent", pa::bf16, PA_DTYPE_BF16, 128, 128, 64, 2, true),
-    PA_CAND("br128_bc64_2stage", pa::bf16, PA_DTYPE_BF16, 128, 128, 64, 2, false),
-    PA_CAND("br256_bc32_2stage_persistent", pa::bf16, PA_DTYPE_BF16, 128, 256, 32, 2, true),
-    PA_CAND("br256_bc128_1stage", pa::bf16, PA_DTYPE_BF16, 128, 256, 128, 1, false),
-    PA_CAND("br256_bc64_1stage", pa::bf16, PA_DTYPE_BF16, 128, 256, 64, 1, false),
-    PA_CAND("br256_bc64_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 256, 64, 2, true),
-    PA_CAND("br64_bc64_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 64, 64, 2, true),
-    PA_CAND("br128_bc32_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 128, 32, 2, true),
-    PA_CAND("br128_bc128_1stage", pa::f16, PA_DTYPE_F16, 64, 128, 128, 1, false),
+    PA_CAND("br128_bc64_2stage_persistent", pa::bf16, PA_DTYPE_BF16, 128, 128, 64, 2, true, 0),
+    PA_CAND("br128_bc64_2stage", pa::bf16, PA_DTYPE_BF16, 128, 128, 64, 2, false, 0),
+    PA_CAND("br256_bc32_2stage_persistent", pa::bf16, PA_DTYPE_BF16, 128, 256, 32, 2, true, 0),
+    PA_CAND("br256_bc128_1stage", pa::bf16, PA_DTYPE_BF16, 128, 256, 128, 1, false, 0),
+    PA_CAND("br256_bc64_1stage", pa::bf16, PA_DTYPE_BF16, 128, 256, 64, 1, false, 0),
+    PA_CAND("br256_bc64_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 256, 64, 2, true, 0),
+    PA_CAND("br64_bc64_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 64, 64, 2, true, 0),
+    PA_CAND("br128_bc32_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 128, 32, 2, true, 0),
+    PA_CAND("br128_bc128_1stage", pa::f16, PA_DTYPE_F16, 64, 128, 128, 1, false, 0),
+    PA_CAND("br128_bc64_2stage_persistent_2wg", pa::f16, PA_DTYPE_F16, 64, 128, 64, 2, true, 2),
 };
 constexpr int kCount = (int)(sizeof(kCandidates) / sizeof(kCandidates[0]));
 
@@ -104,16 +107,19 @@ const char* pa_tiles_label(int index) {
   return c ? c->label : "";
 }
 
-int pa_tiles_describe(int index, int* dtype, int* d, int* br, int* bc, int* stages, int* persistent) {
+int pa_tiles_describe(int index, int* dtype, int* d, int* br, int* bc, int* stages, int* persistent,
+                      int* wgs_per_cu) {
   const Candidate* c = find(index);
   if (!c) return fail(PA_ERR_INVALID, "pa_tiles_describe: no candidate %d (there are %d)", index, kCount);
-  if (!dtype || !d || !br || !bc || !stages || !persistent) return fail(PA_ERR_INVALID, "pa_tiles_describe: null output");
+  if (!dtype || !d || !br || !bc || !stages || !persistent || !wgs_per_cu)
+    return fail(PA_ERR_INVALID, "pa_tiles_describe: null output");
   *dtype = c->dtype;
   *d = c->d;
   *br = c->br;
   *bc = c->bc;
   *stages = c->stages;
   *persistent = c->persistent;
+  *wgs_per_cu = c->wgs_cap;
   return PA_OK;
 }
 
@@ -147,9 +153,12 @@ const char* pa_tiles_kernel(int index, int64_t bh, int64_t n) {
   int grid = (int)std::min<long long>((n + c->br - 1) / c->br * bh, INT_MAX);
   if (c->persistent && c->fn(nullptr, nullptr, nullptr, nullptr, (int)bh, (int)n, nullptr, &grid, true) != hipSuccess)
     grid = 0;   // no device: the grid is unknown
-  snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s> grid %d x %d threads",
+  char cap[48] = "";
+  if (c->wgs_cap > 0) snprintf(cap, sizeof(cap), " (at most %d workgroups per CU)", c->wgs_cap);
+  const bool check = c->dtype == PA_DTYPE_F16 && c->stages == 2;   // as in launch()
+  snprintf(desc, sizeof(desc), "fa_mfma_fwd<%s, D=%d, BM=%d, BN=%d, %d stages, out %s%s%s> grid %d x %d threads%s",
            dt_name[c->dtype], c->d, c->br, c->bc, c->stages, dt_name[c->dtype], c->persistent ? ", persistent" : "",
-           grid, c->br / 32 * pa::kWave);
+           check ? ", packed-max check" : "", grid, c->br / 32 * pa::kWave, cap);
   return desc;
 }
 
