@@ -195,7 +195,6 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   typedef MfmaOStage<D, BM, OutT> OS;
   constexpr int OROW = OS::ROW;
   constexpr int OCR = OS::CHUNKS;
-  constexpr int OPASS = PERSIST ? OS::PASSES : 1;
   constexpr int ORW = OS::ROWS;
   static_assert(32 % OS::PASSES == 0 && (ORW * OCR) % kWave == 0, "O passes: whole rows, whole wave reads");
   __shared__ __attribute__((aligned(16))) unsigned char o_lds[PERSIST ? OS::BYTES : 16];
@@ -262,9 +261,15 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
   // (rows past N read as zero).
   V8 qf[QK_STEPS];
   auto load_q = [&](rsrc_t rs, int row) {
+    // hi * 16 from the lane id read afresh (an asm the compiler cannot merge across the two calls):
+    // held from the prologue to the next block's load, it was the one VGPR the persistent fp16
+    // d = 64 kernel spilled.
+    uint32_t lane_now;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_now));
+    const uint32_t hi16 = (lane_now >> 1) & 16u;
 #pragma unroll
     for (int kk = 0; kk < QK_STEPS; ++kk)
-      qf[kk] = __builtin_bit_cast(V8, load16(rs, (uint32_t)(row * RB + kk * 32 + hi * 16)));
+      qf[kk] = __builtin_bit_cast(V8, load16(rs, (uint32_t)(row * RB + kk * 32) + hi16));
   };
   load_q(q_rs, qrow);
 
