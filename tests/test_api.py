@@ -197,6 +197,24 @@ def test_native_argument_validation_without_gpu():
                       "fused_tc")
 
 
+def test_c_abi_example_builds_and_runs(tmp_path):
+    """The C integration path: tests/native/c_abi_example.c includes both public headers as C99
+    (-Wall -Werror), links against the two libraries with gcc and runs calls that need no GPU."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not installed")
+    lib_dir = os.path.dirname(_native.LIB_PATH)
+    exe = str(tmp_path / "c_abi_example")
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(REPO, "include"),
+                    os.path.join(REPO, "tests", "native", "c_abi_example.c"), "-o", exe, "-L", lib_dir, "-lphantom_attn",
+                    "-lphantom_attn_tiles", f"-Wl,-rpath,{lib_dir}"], check=True)
+    out = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.startswith("c abi ok: phantom_attn")
+
+
 def test_fused_tc_kernel_description_without_gpu():
     """The launch description follows the dispatch table; with no device the persistent launch is
     not chosen (as in pa_fused_tc_fwd), and the setter reports the previous setting."""
