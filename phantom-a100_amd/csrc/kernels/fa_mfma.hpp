@@ -11,8 +11,8 @@
 //    consistent with the numerator (the reference sums the unrounded P). On a row dominated by
 //    one key the rounding of that key's P then cancels in O / l.
 //  * Lazy rescale: m is raised (and O, l multiplied by alpha) only when some row of the wave
-//    would exceed it by more than 2^8; otherwise the stale m is kept and P <= 2^8. The
-//    reference rescales at every tile.
+//    would exceed it by more than 2^8 (2^18 under the fp16 packed-max check, CHECK); otherwise
+//    the stale m is kept and P <= 2^8 (2^18). The reference rescales at every tile.
 //
 // gfx950 design (not a translation of the WMMA kernel):
 //  * Each wave owns 32 query rows. Both products are computed transposed so that every
@@ -56,8 +56,8 @@
 //    V have their own two-stage LDS rings (K is consumed one tile ahead of V); the loads of
 //    K(t+2) and V(t+1) fly during iteration t; one barrier per tile.
 //  * O and l are rescaled only in tiles where some row's max outgrew the reference max by
-//    more than 2^8 (a wave-uniform branch, rare after the first tile); on the fp16 fast path
-//    the rescale runs inside phase A, whose QK MFMAs do not touch O.
+//    more than 2^8, or 2^18 under CHECK (a wave-uniform branch, rare after the first tile); on
+//    the fp16 row-max fast path the rescale runs inside phase A, whose QK MFMAs do not touch O.
 //  * KSPLIT == 2 (short rows on a small grid): the workgroup's waves form two key groups; group
 //    g walks the key tiles g, g + 2, ... through its own half of every LDS stage, with its own
 //    (m, l, O), so each wave walks half the tiles. At the end group 1 hands (m, l, O) to the
