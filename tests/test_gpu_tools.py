@@ -103,3 +103,25 @@ def test_reference_workload_runs_the_harness_protocol():
     assert [r["status"] for r in rows] == ["ok", "ok"]
     for r in rows:
         assert r["median_ms"] > 0 and r["max_abs_err"] <= 2e-3 and r["speedup_vs_a100"] > 0
+
+
+def test_tile_alternatives_compute_attention():
+    """Every candidate of libphantom_attn_tiles.so on a small shape of its dtype and head dim: within
+    the benchmark's gate of float64 attention (fp16 2e-3; bf16 the weights' rounding bound), and the
+    shipped tile held to fewer workgroups per CU bitwise equal to fused_tc's own launch."""
+    from autotune import tile_candidates as tc
+    bm = load("pa_benchmark_gpu3", os.path.join(PKG, "bench", "benchmark.py"))
+    import cuda_attn
+    from autotune import select_tiles as st
+    for c in tc.candidates():
+        b, h, n, d = 2, 3, 512, c["d"]
+        g = torch.Generator().manual_seed(c["index"])
+        q, k, v = (torch.randn(b, h, n, d, generator=g).to(c["dtype"]).cuda() for _ in range(3))
+        print(f"[tiles] {c['label']} {c['dtype']} d={d}: {tc.kernel(c['index'], b * h, n)}", flush=True)
+        out = tc.forward(c["index"], q, k, v)
+        torch.cuda.synchronize()
+        ref32, ref_absv = bm.reference_pair(q, k, v, False)
+        err, ok = bm.gate_against(out, (ref32, ref_absv), q.dtype)
+        assert ok, (c["label"], err)
+        if (c["br"], c["bc"], c["stages"]) == st.TC_TILE[d] and c["persistent"]:
+            assert torch.equal(out, cuda_attn.fused_tc(q, k, v)), c["label"]
