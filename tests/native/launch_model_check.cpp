@@ -9,7 +9,12 @@
 //    CU, as the launcher sizes them.
 // 2. The busiest CU's key tiles under each per-XCD walk, for whole-head shapes, against an
 //    independent restatement, and the walk the launcher then takes.
+// 3. The walk cache: a second call agrees, evicted entries are counted afresh, and eight threads
+//    reading and replacing entries at once all get the uncached answer (the test also builds this
+//    file with ThreadSanitizer on the host code where the toolchain has its runtime).
+#include <atomic>
 #include <cstdio>
+#include <thread>
 #include <vector>
 
 #include "launch_model.hpp"
@@ -104,6 +109,24 @@ int main() {
   }
   // Heads the per-XCD lists may not take walk one list over the device.
   CHECK(pa::causal_walk(16384, 4, 256, 64, 8, 32, false, false) == 2, "B*H=4: walk not the device list");
+  // Eight threads asking for 48 shapes at once (three times what the cache holds, so entries are
+  // evicted while others are read): every answer equals the uncached count.
+  {
+    std::vector<int> want(48);
+    for (int i = 0; i < 48; ++i) want[i] = pa::causal_walk_uncached(2048 + 64 * i, 96, 256, 64, 32, 32);
+    std::atomic<int> wrong{0};
+    std::vector<std::thread> pool;
+    for (int t = 0; t < 8; ++t)
+      pool.emplace_back([&, t] {
+        for (int r = 0; r < 20; ++r)
+          for (int i = 0; i < 48; ++i) {
+            const int j = (i * 7 + t * 5 + r) % 48;
+            if (pa::causal_walk(2048 + 64 * j, 96, 256, 64, 32, 32, false, true) != want[j]) ++wrong;
+          }
+      });
+    for (auto& th : pool) th.join();
+    CHECK(wrong.load() == 0, "threads: %d cached walks differ from the count", wrong.load());
+  }
   std::printf("%s\n", failures ? "FAILED" : "ok");
   return failures ? 1 : 0;
 }
