@@ -115,6 +115,47 @@ def test_large_scores_do_not_overflow(name, scale):
     assert max_err(out, cuda_attn.reference(q, k, v)) < 1e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [30.0, 64.0])
+def test_fused_tc_extreme_score_ranges(dtype, d, causal, scale, per_block_launch):
+    """Q and K scaled by 30 and 64 (scores spread over hundreds of octaves, so nearly every row is
+    one-hot and every tile's lazy check fires or its P underflows), ragged and full N, both launch
+    forms: finite, and within float64 by max(2e-3, R + E), element by element.
+    R = u / (1 - u) (sum_j p_j |V_j| + |O|) bounds the move of O when every weight is rounded to the
+    input dtype (u = 2^-8 bf16, 2^-11 fp16). E covers the fp32 rounding of the scores themselves,
+    which at these magnitudes (|S| ~ 10^4) no summation order avoids: a score off by delta_j scales
+    its weight by exp(delta_j), so O moves by at most sum_j p_j |delta_j - mean_p(delta)| |V_j - O|
+    <= w.|V| + (sum_j w_j) |O| with w_j = p_j |delta_j - mean_p(delta)|; delta is measured on an fp32
+    product of the same inputs (S32 - S64) and doubled for the kernel's own summation order."""
+    u = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[dtype]
+    for n in (1000, 1024):
+        g = torch.Generator().manual_seed(n + d)
+        q, k, v = (torch.randn(2, 4, n, d, generator=g) for _ in range(3))
+        q, k, v = (q * scale).to(dtype), (k * scale).to(dtype), v.to(dtype)
+        qd, kd, vd = (t.double().cuda() for t in (q, k, v))
+        s = qd @ kd.transpose(-1, -2) / d ** 0.5
+        delta = 2 * ((qd.float() @ kd.float().transpose(-1, -2)).double() / d ** 0.5 - s)
+        if causal:
+            s = s.masked_fill(torch.ones(n, n, dtype=torch.bool, device="cuda").triu(1), float("-inf"))
+        p = torch.softmax(s, -1)
+        ref = p @ vd
+        w = p * (delta - (p * delta).sum(-1, keepdim=True)).abs()
+        bound = u / (1 - u) * (p @ vd.abs() + ref.abs()) + w @ vd.abs() + w.sum(-1, keepdim=True) * ref.abs()
+        bar = torch.maximum(torch.full_like(ref, 2e-3), bound)
+        print(f"[extreme] n={n}: bar up to {bar.max().item():.2e}", flush=True)
+        q, k, v = q.cuda(), k.cuda(), v.cuda()
+        for persistent in (True, False):
+            per_block_launch(persistent)
+            print(f"[extreme] {dtype} d={d} causal={causal} scale={scale} n={n} persistent={persistent}", flush=True)
+            out = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            assert torch.isfinite(out).all()
+            err = (out.double() - ref).abs()
+            assert (err <= bar).all(), f"max error {err.max().item():.2e}, worst excess {(err - bar).max().item():.2e}"
+
+
 def test_long_sequence_fused_versions_agree():
     q, k, v = gpu_qkv(1, 2, 8192, 64, torch.float16)
     base = cuda_attn.fused(q, k, v).float()
