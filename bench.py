@@ -10,7 +10,10 @@ HBM. `value` = 4*B*H*N^2*d FLOPs per step x steps / the time of the K steps betw
 synchronisations (HIP events on the launch stream). MI355X raises its clock over the first ~30
 launches of this kernel, so before the warm-up a fixed-duration settle phase (--settle seconds of
 back-to-back calls, reported as `settle`) brings the clock to its steady state; the warm-up and
-the timed steps are exactly --warmup and --steps calls. Every config of the measurement plan is
+the timed steps are exactly --warmup and --steps calls. A host thread samples amdsmi's per-XCD
+shader clocks and the socket power during the settle's last second and during the warm-up and timed
+steps (`clock`; null where amdsmi does not import), so the line can be read against the clock the
+box held under its power cap. Every config of the measurement plan is
 also timed with the reference's protocol (/root/reference/bench/benchmark.py:78-93: warm-ups,
 then per call a flush of a buffer larger than the 256 MB Infinity Cache, event timing,
 median/p10/p90), each after its own settle phase, and reported under "per_config" beside the
