@@ -156,6 +156,31 @@ def test_fused_tc_extreme_score_ranges(dtype, d, causal, scale, per_block_launch
             assert (err <= bar).all(), f"max error {err.max().item():.2e}, worst excess {(err - bar).max().item():.2e}"
 
 
+@pytest.mark.parametrize("name, dtype, bh, n", [
+    ("naive", torch.float32, 65535, 3),       # the unfused paths' grid.y limit
+    ("tiled", torch.float16, 65535, 5),
+    ("fused", torch.float32, 70000, 33),      # 1-D grids past 65535 blocks
+    ("fused_tc", torch.float16, 70000, 64),
+    ("fused_tc", torch.bfloat16, 20000, 200),
+])
+def test_many_heads(name, dtype, bh, n):
+    """B*H at and past 65535 (the y grid dimension of the unfused paths; the fused paths launch
+    1-D grids): every head's output matches the fp32 reference at the reference's bars (fp32 1e-4,
+    fp16 2e-3); bf16 element by element at max(2e-3, u / (1 - u) (sum p|V| + |O|)) + half a bf16 ulp
+    of O, u = 2^-8 (the weights' and the output's rounding to bf16)."""
+    q, k, v = gpu_qkv(1, bh, n, 64, dtype)
+    print(f"[many heads] {name} {dtype} B*H={bh} N={n}", flush=True)
+    out = cuda_attn.KERNELS[name](q, k, v)
+    torch.cuda.synchronize()
+    ref = cuda_attn.reference(q, k, v)
+    if dtype == torch.bfloat16:
+        u = 2.0 ** -8
+        bar = torch.clamp(u / (1 - u) * (cuda_attn.reference(q, k, v.abs()) + ref.abs()), min=2e-3) + u * ref.abs()
+        assert ((out.float() - ref).abs() <= bar).all()
+    else:
+        assert max_err(out, ref) <= TOL[dtype]
+
+
 def test_long_sequence_fused_versions_agree():
     q, k, v = gpu_qkv(1, 2, 8192, 64, torch.float16)
     base = cuda_attn.fused(q, k, v).float()
