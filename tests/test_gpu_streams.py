@@ -6,6 +6,8 @@ asynchronously, `attn_*.cu`; here `cuda_attn` passes `torch.cuda.current_stream(
 * A launch consumes inputs produced on the same side stream just before it, with no extra sync.
 * The fused entry points can be captured in a HIP graph; every replay (with new inputs copied in
   eagerly between replays) matches the eager result bit for bit.
+* Eight host threads calling the library at once, each on its own stream, get the same bits and
+  their own error messages.
 All streams keep the default priority.
 """
 from __future__ import annotations
@@ -102,3 +104,50 @@ def test_graph_capture_replays_match_eager(name, shape, dtype, causal, kw):
         want = fn(nq, nk, nv, causal, **kw)       # eager, between replays
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {replay}"
+
+
+def test_host_threads_call_concurrently():
+    """Eight host threads, each on its own stream, call fused_tc concurrently (ctypes releases the
+    GIL in the library call) on shapes that exercise the launch caches: causal shapes whose walk is
+    counted and cached, non-causal persistent and key-split shapes; between calls each thread makes
+    a rejected call and reads back its own error message (per-thread). Every output equals the same
+    call made alone on the default stream."""
+    import threading
+
+    from cuda_attn import _native
+    shapes = [((2, 8, 1024, 128), torch.bfloat16, True), ((1, 12, 2048, 128), torch.bfloat16, True),
+              ((2, 8, 512, 64), torch.float16, True), ((2, 8, 1000, 64), torch.float16, False),
+              ((1, 42, 128, 64), torch.float16, False), ((2, 16, 768, 128), torch.bfloat16, False)]
+    inputs = [(make_qkv(*shp, dt, seed=80 + i, device="cuda"), causal) for i, (shp, dt, causal) in enumerate(shapes)]
+    want = [cuda_attn.fused_tc(q, k, v, causal) for (q, k, v), causal in inputs]
+    torch.cuda.synchronize()
+    failures = []
+
+    def worker(t):
+        stream = torch.cuda.Stream()
+        p = 256
+        try:
+            for r in range(6):
+                for j in range(len(inputs)):
+                    i = (j + t + r) % len(inputs)
+                    (q, k, v), causal = inputs[i]
+                    with torch.cuda.stream(stream):
+                        out = cuda_attn.fused_tc(q, k, v, causal)
+                    stream.synchronize()
+                    if not torch.equal(out, want[i]):
+                        failures.append(f"thread {t}: case {i} differs")
+                    d = 96 + 16 * (t % 2)   # 96 and 112: uncompiled head dims, rejected before any launch
+                    rc = _native.lib().pa_fused_tc_fwd(p, p, p, p, _native.DTYPE_F16, _native.DTYPE_F16, 1, 64, d, 0, None)
+                    msg = _native.last_error()
+                    if rc != _native.ERR_UNSUPPORTED or f"(got {d})" not in msg:
+                        failures.append(f"thread {t}: rc {rc}, message {msg!r}")
+        except Exception as e:   # noqa: BLE001 - reported below
+            failures.append(f"thread {t}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(8)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert not failures, failures[:5]
