@@ -160,7 +160,9 @@ def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = F
     for short d = 64 rows on a small grid; otherwise one workgroup per query block.
     cuda_attn._native.fused_tc_kernel names the launch a call takes. PA_PERSISTENT=0 in the
     environment when the library loads, or cuda_attn._native.set_persistent(False), selects one
-    workgroup per query block instead of the persistent launch (same bits)."""
+    workgroup per query block instead of the persistent launch (same bits, except for fp16 at d = 64
+    on non-causal rows: the persistent kernel starts a rescale on the packed maximum of the rounded
+    probabilities, the per-block one on the row maximum; both within the fp16 bar)."""
     _checks.check_inputs(q, k, v)
     _checks.check_tc(q, k, v)
     od = _checks.resolve_out_dtype("fused_tc", q, out_dtype)
