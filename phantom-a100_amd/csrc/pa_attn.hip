@@ -271,18 +271,22 @@ const MfmaEntry kTcTable[] = {
     PA_TC_BOTH_OUT(pa::f16, 128, 256, 64, 2),
     PA_TC_BOTH_OUT(pa::bf16, 128, 256, 64, 2),
 };
-// Short rows on a small grid (d = 64, 2-4 key tiles, at most one workgroup per CU): 64-query
-// workgroups whose keys are split over two groups of 2 waves, so each wave walks half the tiles
-// and the extra waves land on otherwise idle CUs; the groups merge at the end. Measured at
-// BH = 42: N = 128 7.76 vs 8.44 us, N = 256 9.48 vs 10.16 us; slower with one tile, longer rows or
-// a grid that already fills the chip.
+// Small grids at d = 64: 64-query workgroups whose keys are split over two groups of 2 waves, so
+// each wave walks half the tiles and the extra waves land on otherwise idle CUs; the groups merge
+// at the end. Taken for rows of 2-4 key tiles with at most one such workgroup per CU (measured at
+// BH = 42: N = 128 7.76 vs 8.44 us, N = 256 9.48 vs 10.16 us), and for rows of any length whose
+// 128-query blocks fill at most half the CUs: back to back against the persistent launch, fp16,
+// B*H x N from 1 x 512 to 32 x 512, 1 x 16384 and 2 x 8192, time ratio 0.85-0.92 non-causal and
+// 0.79-0.83 causal; at 256 such blocks it lost non-causal (1.12-1.17) and mostly causal (1.02-1.04
+// for N <= 2048). Slower with one tile or a grid that already fills the chip.
 constexpr int kCUs = 256;   // MI355X / gfx950
 const MfmaEntry kTcSplitTable[] = {
     PA_TC_SPLIT_BOTH_OUT(pa::f16, 64, 64, 64),
     PA_TC_SPLIT_BOTH_OUT(pa::bf16, 64, 64, 64),
 };
 bool use_key_split(int64_t d, int64_t n, int64_t bh) {
-  return d == 64 && n > 64 && n <= 256 && (n + 63) / 64 * bh <= kCUs;
+  if (d != 64 || n <= 64) return false;
+  return (n <= 256 && (n + 63) / 64 * bh <= kCUs) || (n + 127) / 128 * bh <= kCUs / 2;
 }
 
 // fused_tuned: the reference's tile sweep set (fused_tuned.cuh:207) x {one, two} LDS stages.

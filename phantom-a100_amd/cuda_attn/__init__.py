@@ -156,8 +156,9 @@ def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = F
     """v4: both matmuls on MFMA (fp16/bf16 in, fp32 accumulate), online softmax in between.
     FP16 or BF16, d in {64, 128}. The library picks the launch from the shape: persistent (as many
     workgroups as fit at once, walking the query blocks) for every causal call and for non-causal
-    calls with an even number of 64-key tiles or an odd number, above one, of full ones; a key split
-    for short d = 64 rows on a small grid; otherwise one workgroup per query block.
+    calls with an even number of 64-key tiles or an odd number, above one, of full ones; at d = 64 a
+    key split instead where the grid is small (rows of 2-4 key tiles, or 128-query blocks that fill
+    at most half the CUs); otherwise one workgroup per query block.
     cuda_attn._native.fused_tc_kernel names the launch a call takes. PA_PERSISTENT=0 in the
     environment when the library loads, or cuda_attn._native.set_persistent(False), selects one
     workgroup per query block instead of the persistent launch (same bits, except for fp16 at d = 64

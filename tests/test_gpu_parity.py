@@ -631,8 +631,8 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((8, 16, 1024), torch.float16, 1.0, None, 64),
     ((1, 16, 8192), torch.float16, 3.0, torch.float32, 64),
     ((4, 64, 128), torch.bfloat16, 1.0, torch.float32, 64),
-    ((2, 8, 384), torch.bfloat16, 3.0, None, 64),
-    ((2, 8, 640), torch.float16, 10.0, torch.float32, 64),
+    ((2, 24, 384), torch.bfloat16, 3.0, None, 64),   # (at d = 64, fewer heads take the key split)
+    ((2, 16, 640), torch.float16, 10.0, torch.float32, 64),
     # B*H not a multiple of 8 (some XCDs own one head more), at least one block per workgroup
     ((1, 100, 1024), torch.bfloat16, 1.0, None, 128),
     ((3, 27, 2048), torch.float16, 3.0, torch.float32, 64),
@@ -646,7 +646,7 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((1, 16, 20), torch.bfloat16, 1.0, torch.float32, 128),   # one partial tile, padded to 2
     ((4, 8, 1030), torch.float16, 3.0, None, 64),           # 17 tiles, padded to 18
     ((4, 64, 100), torch.bfloat16, 1.0, None, 64),
-    ((2, 8, 1000), torch.float16, 1.0, torch.float32, 64),
+    ((2, 12, 1000), torch.float16, 1.0, torch.float32, 64),
     ((1, 42, 4000), torch.bfloat16, 1.0, torch.float32, 128),  # and uneven heads per XCD
     # d = 128 walks by length where head by head leaves some CU above the others
     ((2, 16, 3072), torch.bfloat16, 1.0, None, 128),
@@ -655,7 +655,7 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((1, 4, 4096), torch.bfloat16, 1.0, None, 128),
     ((1, 12, 1024), torch.bfloat16, 1.0, torch.float32, 128),
     ((1, 1, 1000), torch.bfloat16, 3.0, None, 128),
-    ((1, 3, 2048), torch.float16, 3.0, torch.float32, 64),
+    ((1, 9, 2048), torch.float16, 3.0, torch.float32, 64),
     ((2, 5, 3000), torch.float16, 1.0, None, 64),
     ((1, 6, 4096), torch.bfloat16, 1.0, None, 64),
     # extremes: one query, many heads of one short tile, a row one past a tile
@@ -757,9 +757,11 @@ BOUNDS_CASES = [  # (B, H, N), dtype, d, causal, persistent launch
     ((2, 8, 4032), torch.bfloat16, 64, False, True),    # RAGGED: 63 full tiles, padded to 64
     ((2, 8, 1000), torch.bfloat16, 128, True, True),    # causal persistent, last block past N
     ((1, 8, 20), torch.bfloat16, 128, True, True),      # causal persistent, N below one tile
-    ((1, 8, 1030), torch.float16, 64, True, True),      # causal persistent, 17 tiles padded to 18
+    ((2, 12, 1030), torch.float16, 64, True, True),     # causal persistent, 17 tiles padded to 18
     ((2, 8, 1000), torch.bfloat16, 128, True, False),   # per-block launch
-    ((2, 8, 1000), torch.float16, 64, False, False),
+    ((2, 12, 1000), torch.float16, 64, False, False),
+    ((1, 4, 1030), torch.float16, 64, True, False),     # key split on a small grid, causal, last tile partial
+    ((1, 2, 1000), torch.bfloat16, 64, False, False),   # key split on a small grid
 ]
 
 
@@ -836,6 +838,35 @@ def test_key_split_matches_unsplit(n, dtype, causal):
     assert max_err(small, ref) <= tol and max_err(big, ref) <= tol
     assert np.abs(small[0].cpu().numpy() - online).max() <= tol
     assert max_err(small, big) <= tol
+
+
+@pytest.mark.parametrize("n, heads", [(1000, 2), (1024, 16), (4096, 4), (8192, 1)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_key_split_on_small_grids(n, heads, dtype, causal):
+    """d = 64 rows of any length whose 128-query blocks fill at most half the CUs take the key-split
+    kernel; the same heads inside a batch that fills the chip take the persistent one. On the first
+    and last 128 rows of the first and last head, both match float64 and the reference algorithm
+    at 2e-3 (wider only where the reference algorithm itself misses float64 by more)."""
+    print(f"[key split, small grid] n={n} heads={heads} {dtype} causal={causal}", flush=True)
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    assert "key split 2" in _native.fused_tc_kernel(code, _native.DTYPE_F32, heads, n, 64, causal)
+    assert "key split" not in _native.fused_tc_kernel(code, _native.DTYPE_F32, 256, n, 64, causal)
+    q, k, v = make_qkv(1, 256, n, 64, dtype, seed=43, device="cuda")
+    big = cuda_attn.fused_tc(q, k, v, causal, out_dtype=torch.float32)[:, :heads]
+    qs, ks, vs = (t[:, :heads].contiguous() for t in (q, k, v))
+    small = cuda_attn.fused_tc(qs, ks, vs, causal, out_dtype=torch.float32)
+    for head in sorted({0, heads - 1}):
+        qn, kn, vn = (t[:, head:head + 1].float().cpu().numpy()[0] for t in (qs, ks, vs))
+        for lo, hi in ((0, 128), ((n - 128) // 128 * 128, n)):   # tiles of the reference (br 64, 128)
+            rows = torch.arange(lo, hi, device="cuda")
+            ref = f64_rows_gpu(qs, ks, vs, head, rows, causal)
+            tol, e_ref, online = pb.reference_bar(qn, kn, vn, causal, dtype, ref[None].cpu().numpy(), q_rows=(lo, hi))
+            print(f"  head {head} rows {lo}-{hi}: bar {tol:.2e} (reference algorithm vs float64 {e_ref:.2e})", flush=True)
+            for out in (small, big):
+                got = out[0, head, lo:hi]
+                assert max_err(got, ref) <= tol
+                assert np.abs(got.cpu().numpy() - online[0]).max() <= tol
 
 
 def f64_rows_gpu(q, k, v, head, rows, causal):
