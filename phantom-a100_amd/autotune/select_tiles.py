@@ -48,7 +48,9 @@ RUN_ONE = os.path.join(_PKG, "bench", "run_one.py")
 RESOURCES = os.path.join(_PKG, "cuda_attn", "kernel_resources.json")
 DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16}
 MANGLED_T = {torch.float16: "DF16_", torch.bfloat16: "DF16b", torch.float32: "f"}
-# fused_tc's compiled tile per head dim (the launch table in csrc/pa_attn.hip).
+# fused_tc's general tile per head dim (the launch table in csrc/pa_attn.hip). On small grids the
+# library takes another launch (d = 64: a key split; d = 128: 128-query workgroups); the report's
+# launch column names it, and its resources are looked up for the tile that launch uses.
 TC_TILE = {64: (128, 64, 2), 128: (256, 64, 2)}
 
 
@@ -102,9 +104,12 @@ def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal:
     # fp16 two-stage tiles on non-causal rows use the packed-max check in fused_tc's persistent
     # forms, at d = 128 per block, and in every alternative; both launchers name it
     check = ", packed-max check" in desc
+    tile = re.search(r"BM=(\d+), BN=(\d+), (\d) stages", desc)
     return {"ksplit": 2 if "key split 2" in desc else 1, "persistent": ", persistent" in desc,
             "ragged": ", ragged" in desc, "causal": ", persistent, causal" in desc, "check": check,
-            "workgroups": int(grid.group(1)) if grid else -(-n // br) * bh, "description": desc}
+            "workgroups": int(grid.group(1)) if grid else -(-n // br) * bh, "description": desc,
+            # the tile the launch uses (fused_tc takes a smaller one on small grids)
+            "tile": tuple(int(x) for x in tile.groups()) if tile else None}
 
 
 def load_resources(path: str = RESOURCES) -> dict:
@@ -217,10 +222,11 @@ def evaluate(args) -> list[dict]:
         med, p10, p90 = time_calls(fn, 5, args.iters, flush)
         row.update(status="ok", median_ms=med, p10_ms=p10, p90_ms=p90, tflops=flops / (med * 1e-3) / 1e12)
         form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br, source)
-        res = find_resources(res_all, kernel_key(dt, args.dim, br, bc, st, dt, form["ksplit"], form["persistent"],
+        kbr, kbc, kst = form["tile"] or (br, bc, st)
+        res = find_resources(res_all, kernel_key(dt, args.dim, kbr, kbc, kst, dt, form["ksplit"], form["persistent"],
                                                  form["ragged"], form["causal"], form["check"]))
         row["launch"] = form["description"]
-        threads = br // 32 * 64 * form["ksplit"]   # one wave per 32 query rows per key group
+        threads = kbr // 32 * 64 * form["ksplit"]   # one wave per 32 query rows per key group
         if res:
             waves, lim = hc.theoretical_waves_per_simd(res["vgprs"], res["agprs"], res["lds_bytes"], threads)
             row.update(regs=res["vgprs"] + res["agprs"], waves_per_simd_limit=waves, occupancy_limiter=lim,
