@@ -90,7 +90,7 @@ def launch_form(entry: str, dtype: torch.dtype, d: int, n: int, bh: int, causal:
     pa_tiles_kernel for an alternative), so the report names the kernel that actually runs."""
     if entry != "fused_tc":
         return {"ksplit": 1, "persistent": False, "ragged": False, "causal": False, "check": False,
-                "workgroups": -(-n // br) * bh, "description": ""}
+                "workgroups": -(-n // br) * bh, "description": "", "tile": None}
     if isinstance(source, int):
         desc = tc.kernel(source, bh, n)
     else:
@@ -222,7 +222,7 @@ def evaluate(args) -> list[dict]:
         med, p10, p90 = time_calls(fn, 5, args.iters, flush)
         row.update(status="ok", median_ms=med, p10_ms=p10, p90_ms=p90, tflops=flops / (med * 1e-3) / 1e12)
         form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br, source)
-        kbr, kbc, kst = form["tile"] or (br, bc, st)
+        kbr, kbc, kst = form.get("tile") or (br, bc, st)
         res = find_resources(res_all, kernel_key(dt, args.dim, kbr, kbc, kst, dt, form["ksplit"], form["persistent"],
                                                  form["ragged"], form["causal"], form["check"]))
         row["launch"] = form["description"]
