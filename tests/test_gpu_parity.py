@@ -879,19 +879,20 @@ def test_key_split_on_small_grids(n, heads, dtype, causal):
 @pytest.mark.parametrize("n, heads, dtype, out_dtype", [
     (2048, 8, torch.bfloat16, None), (1024, 16, torch.float16, torch.float32), (1000, 8, torch.bfloat16, None),
     (1030, 4, torch.float16, None), (8192, 1, torch.float16, torch.float32), (100, 40, torch.bfloat16, None)])
-def test_small_grid_tile_matches_the_256_query_tile(n, heads, dtype, out_dtype):
-    """d = 128, non-causal, 256-query blocks filling at most half the CUs: the 128-query tile (two
-    workgroups per CU) computes each 32-query wave exactly as the 256-query tile does, so the same
-    heads inside a batch that takes the 256-query tile give the same bits."""
+@pytest.mark.parametrize("causal", [False, True])
+def test_small_grid_tile_matches_the_256_query_tile(n, heads, dtype, out_dtype, causal):
+    """d = 128, 256-query blocks filling at most half the CUs: the 128-query tile (two workgroups
+    per CU) computes each 32-query wave exactly as the 256-query tile does, so the same heads inside
+    a batch that takes the 256-query tile give the same bits, causal or not."""
     code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
     od = code if out_dtype is None else _native.DTYPE_F32
-    desc_small = _native.fused_tc_kernel(code, od, heads, n, 128, False)
-    desc_big = _native.fused_tc_kernel(code, od, 256, n, 128, False)
-    print(f"[small grid] n={n} heads={heads} {dtype}: {desc_small} / {desc_big}", flush=True)
+    desc_small = _native.fused_tc_kernel(code, od, heads, n, 128, causal)
+    desc_big = _native.fused_tc_kernel(code, od, 256, n, 128, causal)
+    print(f"[small grid] n={n} heads={heads} {dtype} causal={causal}: {desc_small} / {desc_big}", flush=True)
     assert "BM=128" in desc_small and "BM=256" in desc_big
     q, k, v = make_qkv(1, 256, n, 128, dtype, seed=44, device="cuda")
-    big = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)[:, :heads]
-    small = cuda_attn.fused_tc(*(t[:, :heads].contiguous() for t in (q, k, v)), out_dtype=out_dtype)
+    big = cuda_attn.fused_tc(q, k, v, causal, out_dtype=out_dtype)[:, :heads]
+    small = cuda_attn.fused_tc(*(t[:, :heads].contiguous() for t in (q, k, v)), causal, out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert torch.equal(small, big)
 
