@@ -277,16 +277,20 @@ const MfmaEntry kTcTable[] = {
 // BH = 42: N = 128 7.76 vs 8.44 us, N = 256 9.48 vs 10.16 us), and for rows of any length whose
 // 128-query blocks fill at most half the CUs: back to back against the persistent launch, fp16,
 // B*H x N from 1 x 512 to 32 x 512, 1 x 16384 and 2 x 8192, time ratio 0.85-0.92 non-causal and
-// 0.79-0.83 causal; at 256 such blocks it lost non-causal (1.12-1.17) and mostly causal (1.02-1.04
-// for N <= 2048). Slower with one tile or a grid that already fills the chip.
+// 0.79-0.83 causal. Causal rows of 4096 keys or more keep it up to one such block per CU (their
+// blocks' lengths differ, so the longest one bounds the launch): 6x4096 0.92, 5x4096 (bf16) 0.94,
+// 7x4096 0.92, 4x8192 0.86, 2x16384 1.00, 1x8x4096 0.83; between half and all of the CUs it lost
+// non-causal (1.13-1.20) and tied or lost causal at shorter rows (28x1024 1.00, 1x16x2048 1.03).
+// Slower with one tile or a grid that already fills the chip.
 constexpr int kCUs = 256;   // MI355X / gfx950
 const MfmaEntry kTcSplitTable[] = {
     PA_TC_SPLIT_BOTH_OUT(pa::f16, 64, 64, 64),
     PA_TC_SPLIT_BOTH_OUT(pa::bf16, 64, 64, 64),
 };
-bool use_key_split(int64_t d, int64_t n, int64_t bh) {
+bool use_key_split(int64_t d, int64_t n, int64_t bh, int causal) {
   if (d != 64 || n <= 64) return false;
-  return (n <= 256 && (n + 63) / 64 * bh <= kCUs) || (n + 127) / 128 * bh <= kCUs / 2;
+  const int64_t blocks = (n + 127) / 128 * bh;
+  return (n <= 256 && (n + 63) / 64 * bh <= kCUs) || blocks <= kCUs / 2 || (causal && n >= 4096 && blocks <= kCUs);
 }
 // Small grids at d = 128: 128-query workgroups (4 waves, two per CU) where the 256-query blocks
 // would fill at most half the CUs, so the work spreads over twice the CUs; every wave computes
@@ -294,25 +298,27 @@ bool use_key_split(int64_t d, int64_t n, int64_t bh) {
 // TFLOP/s, non-causal bf16: 1x8x1024 176 -> 234, 1x16x1024 356 -> 458, 1x32x1024 687 -> 813,
 // 1x16x2048 833 -> 954, 1x4x4096 467 -> 629, 2x8x2048 813 -> 948, 1x2x8192 489 -> 654, 1x64x512
 // 534 -> 652; causal: bf16 1x8x2048 203 -> 277, 1x16x1024 171 -> 222, 1x4x4096 227 -> 322, 1x8x1000
-// 82 -> 109, fp16 1x2x8192 197 -> 284, 1x32x1024 290 -> 373. At 256 such blocks it lost
-// (non-causal bf16 2x32x1024 1008 -> 957) or tied (causal bf16 2x16x2048 711 -> 716).
+// 82 -> 109, fp16 1x2x8192 197 -> 284, 1x32x1024 290 -> 373. Causal rows keep it up to one such
+// block per CU (bf16 12x4096 645 -> 828, 10x4096 550 -> 719, 28x2048 632 -> 704, 16x4096 763 ->
+// 937, 2x16x2048 711 -> 716; fp16 14x4096 626 -> 733); non-causal between half and all of the CUs
+// it lost (bf16 40x1024 795 -> 724, 48x1024 873 -> 801, 2x32x1024 1008 -> 957).
 const MfmaEntry kTcSmallGridTable[] = {
     PA_TC_BOTH_OUT(pa::f16, 128, 128, 64, 2),
     PA_TC_BOTH_OUT(pa::bf16, 128, 128, 64, 2),
 };
-bool use_small_grid_tile(int64_t d, int64_t n, int64_t bh) {
-  return d == 128 && (n + 255) / 256 * bh <= kCUs / 2;
+bool use_small_grid_tile(int64_t d, int64_t n, int64_t bh, int causal) {
+  return d == 128 && (n + 255) / 256 * bh <= (causal ? kCUs : kCUs / 2);
 }
 
 // fused_tuned: the reference's tile sweep set (fused_tuned.cuh:207) x {one, two} LDS stages.
 #define PA_TUNED(BR, BC) PA_TUNED_BOTH_OUT(pa::f16, 64, BR, BC, 1), PA_TUNED_BOTH_OUT(pa::f16, 64, BR, BC, 2)
 const MfmaEntry kTunedTable[] = {PA_TUNED(64, 32), PA_TUNED(64, 64), PA_TUNED(128, 32), PA_TUNED(128, 64)};
 
-const MfmaEntry* find_tc(int dtype, int out_dtype, int64_t d, int64_t n, int64_t bh) {
-  if (use_key_split(d, n, bh))
+const MfmaEntry* find_tc(int dtype, int out_dtype, int64_t d, int64_t n, int64_t bh, int causal) {
+  if (use_key_split(d, n, bh, causal))
     for (const auto& e : kTcSplitTable)
       if (e.dtype == dtype && e.out_dtype == out_dtype && e.d == d) return &e;
-  if (use_small_grid_tile(d, n, bh))
+  if (use_small_grid_tile(d, n, bh, causal))
     for (const auto& e : kTcSmallGridTable)
       if (e.dtype == dtype && e.out_dtype == out_dtype && e.d == d) return &e;
   for (const auto& e : kTcTable)
@@ -567,14 +573,14 @@ int pa_fused_tc_fwd(const void* q, const void* k, const void* v, void* o, int dt
     return fail(PA_ERR_UNSUPPORTED, "%s: only head dimensions 64 and 128 are compiled (got %lld)", name, (long long)d);
   if (int rc = check_aligned16(name, q, k, v, o)) return rc;
   if (int rc = check_head_bytes(name, n, d, dtype)) return rc;
-  const MfmaEntry* e = find_tc(dtype, out_dtype, d, n, bh);
+  const MfmaEntry* e = find_tc(dtype, out_dtype, d, n, bh, causal);
   if (!e) return fail(PA_ERR_UNSUPPORTED, "%s: output dtype must be the input dtype or float32", name);
   return hip_status(e->fn(q, k, v, o, (int)bh, (int)n, causal, static_cast<hipStream_t>(stream)), name);
 }
 
 const char* pa_fused_tc_kernel(int dtype, int out_dtype, int64_t bh, int64_t n, int64_t d, int causal) {
   thread_local char desc[256];
-  const MfmaEntry* e = (bh > 0 && n > 0) ? find_tc(dtype, out_dtype, d, n, bh) : nullptr;
+  const MfmaEntry* e = (bh > 0 && n > 0) ? find_tc(dtype, out_dtype, d, n, bh, causal) : nullptr;
   if (!e) return "";
   static const char* dt_name[] = {"f32", "f16", "bf16"};
   const long long total = (n + e->br - 1) / e->br * bh;
@@ -601,8 +607,8 @@ int64_t pa_fused_tuned_lds_bytes(int br, int bc, int double_buffer, int64_t d, i
 
 int64_t pa_fused_tc_lds_bytes(int64_t d, int dtype) {
   // the larger of the general and the short-row (key-split) tile
-  const MfmaEntry* e = find_tc(dtype, dtype, d, 1 << 20, 1024);
-  const MfmaEntry* s = find_tc(dtype, dtype, d, 128, 1);
+  const MfmaEntry* e = find_tc(dtype, dtype, d, 1 << 20, 1024, 0);
+  const MfmaEntry* s = find_tc(dtype, dtype, d, 128, 1, 0);
   if (!e) return -1;
   return s && s->lds > e->lds ? s->lds : e->lds;
 }

@@ -662,7 +662,7 @@ CAUSAL_PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype, d
     ((1, 1, 1000), torch.bfloat16, 3.0, None, 128),
     ((1, 9, 2048), torch.float16, 3.0, torch.float32, 64),
     ((2, 5, 3000), torch.float16, 1.0, None, 64),
-    ((1, 6, 4096), torch.bfloat16, 1.0, None, 64),
+    ((1, 12, 4096), torch.bfloat16, 1.0, None, 64),   # (fewer heads take the key split)
     # extremes: one query, many heads of one short tile, a row one past a tile
     ((1, 1, 1), torch.bfloat16, 1.0, torch.float32, 128),
     ((64, 64, 16), torch.float16, 3.0, None, 64),
@@ -887,10 +887,10 @@ def test_small_grid_tile_matches_the_256_query_tile(n, heads, dtype, out_dtype, 
     code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
     od = code if out_dtype is None else _native.DTYPE_F32
     desc_small = _native.fused_tc_kernel(code, od, heads, n, 128, causal)
-    desc_big = _native.fused_tc_kernel(code, od, 256, n, 128, causal)
+    desc_big = _native.fused_tc_kernel(code, od, 384, n, 128, causal)
     print(f"[small grid] n={n} heads={heads} {dtype} causal={causal}: {desc_small} / {desc_big}", flush=True)
     assert "BM=128" in desc_small and "BM=256" in desc_big
-    q, k, v = make_qkv(1, 256, n, 128, dtype, seed=44, device="cuda")
+    q, k, v = make_qkv(1, 384, n, 128, dtype, seed=44, device="cuda")
     big = cuda_attn.fused_tc(q, k, v, causal, out_dtype=out_dtype)[:, :heads]
     small = cuda_attn.fused_tc(*(t[:, :heads].contiguous() for t in (q, k, v)), causal, out_dtype=out_dtype)
     torch.cuda.synchronize()
@@ -916,11 +916,12 @@ LONG_ROWS = [  # (N, d, dtype)
 ]
 
 
-@pytest.mark.parametrize("bh", [42, 12, 20])
+@pytest.mark.parametrize("bh", [28, 12, 20])
 def test_causal_with_uneven_heads_per_xcd_takes_the_device_list(bh):
     """Causal B*H not a multiple of 8 whose whole heads per XCD would leave an XCD more than 25 %
-    above the mean (12), or some XCD with fewer blocks than workgroups (42 and 20 at N = 1024,
-    d = 128), walks one list over the device, and still matches float64."""
+    above the mean (12), or some XCD with fewer blocks than workgroups (28 and 20 at N = 1024,
+    d = 128, on the 128-query small-grid tile), walks one list over the device, and still matches
+    float64."""
     desc = _native.fused_tc_kernel(_native.DTYPE_BF16, _native.DTYPE_F32, bh, 1024, 128, True)
     assert "persistent, causal, device list" in desc, desc
     q, k, v = make_qkv(1, bh, 1024, 128, torch.bfloat16, seed=9, device="cuda")
