@@ -301,13 +301,28 @@ bool use_key_split(int64_t d, int64_t n, int64_t bh, int causal) {
 // 82 -> 109, fp16 1x2x8192 197 -> 284, 1x32x1024 290 -> 373. Causal rows keep it up to one such
 // block per CU (bf16 12x4096 645 -> 828, 10x4096 550 -> 719, 28x2048 632 -> 704, 16x4096 763 ->
 // 937, 2x16x2048 711 -> 716; fp16 14x4096 626 -> 733); non-causal between half and all of the CUs
-// it lost (bf16 40x1024 795 -> 724, 48x1024 873 -> 801, 2x32x1024 1008 -> 957).
+// it lost (bf16 40x1024 795 -> 724, 48x1024 873 -> 801, 2x32x1024 1008 -> 957). Non-causal beyond
+// one round of 256-query blocks it wins where the last round is far from full (rounds R, idle
+// share of the launch 1 - R / ceil(R)): bf16 1x72x1024 (R 1.125) 724 -> 845, 1x20x4096 (1.25) 955
+// -> 1078, 3x32x1024 (1.5) 883 -> 1005, 1x36x4096 (2.25) 1081 -> 1161, 1x18x8192 (2.25) 1104 ->
+// 1180, 5x16x2048 (2.5) 1108 -> 1163, 1x80x2048 (2.5) 1119 -> 1171; fp16 1x24x4096 (1.5) 1055 ->
+// 1100, 1x144x1024 (2.25) 822 -> 910; and loses where it is nearly full or full: 1x112x1024 (1.75)
+// 1005 -> 950, 1x56x4096 (3.5) 1216 -> 1221, 2x32x2048 (2) 1128 -> 1068, C4 (8) 1290 -> 1195.
+// Causal rows beyond one round lost with it (3x32x2048 970 -> 863, 1x40x4096 1070 -> 975).
 const MfmaEntry kTcSmallGridTable[] = {
     PA_TC_BOTH_OUT(pa::f16, 128, 128, 64, 2),
     PA_TC_BOTH_OUT(pa::bf16, 128, 128, 64, 2),
 };
 bool use_small_grid_tile(int64_t d, int64_t n, int64_t bh, int causal) {
-  return d == 128 && (n + 255) / 256 * bh <= (causal ? kCUs : kCUs / 2);
+  if (d != 128) return false;
+  const int64_t blocks = (n + 255) / 256 * bh;   // 256-query blocks, one workgroup per CU at a time
+  if (causal) return blocks <= kCUs;
+  if (blocks <= kCUs / 2) return true;
+  if (blocks <= kCUs) return false;
+  // More than one round of 256-query blocks: the 128-query tile where the last round would leave at
+  // least 15 % of the launch's CU time idle (its half-size blocks fill that round's CUs better).
+  const int64_t rounds = (blocks + kCUs - 1) / kCUs, last = blocks - (rounds - 1) * kCUs;
+  return 100 * (kCUs - last) >= 15 * rounds * kCUs;
 }
 
 // fused_tuned: the reference's tile sweep set (fused_tuned.cuh:207) x {one, two} LDS stages.

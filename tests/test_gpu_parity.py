@@ -514,24 +514,27 @@ PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype; d = 128
     ((1, 5, 1024), torch.float16, 1.0, None),
     ((1, 304, 128), torch.float16, 1.0, torch.float32),
     ((2, 40, 1024), torch.float16, 10.0, torch.float32),
-    ((2, 40, 1000), torch.bfloat16, 1.0, None),          # ragged: last tile 40 keys
+    ((2, 64, 1000), torch.bfloat16, 1.0, None),          # ragged: last tile 40 keys
     ((1, 160, 100), torch.bfloat16, 3.0, torch.float32), # ragged, two tiles
     ((4, 32, 4032), torch.bfloat16, 1.0, None),          # 63 full tiles, padded to 64
-    ((2, 40, 960), torch.float16, 3.0, torch.float32),   # 15 full tiles
+    ((2, 64, 960), torch.float16, 3.0, torch.float32),   # 15 full tiles
     ((1, 160, 192), torch.bfloat16, 10.0, torch.float32), # 3 tiles, rescaling rows
-    ((2, 40, 1000), torch.float16, 1.0, torch.float32),
+    ((2, 64, 1000), torch.float16, 1.0, torch.float32),
     ((1, 160, 100), torch.float16, 3.0, None),
     # small grids (256-query blocks filling at most half the CUs): the 128-query tile, two
     # workgroups per CU
     ((1, 8, 2048), torch.bfloat16, 1.0, None),
     ((1, 16, 1024), torch.float16, 3.0, torch.float32),
     ((1, 2, 8192), torch.bfloat16, 1.0, torch.float32),
+    # mid grids whose last round of 256-query blocks is far from full: the 128-query tile
+    ((1, 72, 1024), torch.bfloat16, 1.0, None),
+    ((1, 20, 4096), torch.float16, 1.0, torch.float32),
     ((4, 32, 4050), torch.bfloat16, 1.0, None),          # ragged, 2048 blocks: 8 per workgroup
     ((16, 16, 1000), torch.bfloat16, 1.0, torch.float32),  # ragged, 1024 blocks
-    ((1, 600, 100), torch.bfloat16, 3.0, None),          # ragged, two tiles, 600 blocks
+    ((1, 752, 100), torch.bfloat16, 3.0, None),          # ragged, two tiles, 752 blocks
     ((4, 32, 4050), torch.float16, 1.0, torch.float32),
     ((16, 16, 1000), torch.float16, 1.0, None),
-    ((1, 600, 100), torch.float16, 3.0, torch.float32),
+    ((1, 752, 100), torch.float16, 3.0, torch.float32),
 ]
 
 
@@ -758,7 +761,8 @@ def test_causal_persistent_form_matches_per_block_form(shape, dtype, qk_scale, o
 # the tail would put NaN into O through P.V (0 * NaN = NaN). The tails are longer than any tile a
 # launch reads past N, so every access stays inside the allocation either way.
 BOUNDS_CASES = [  # (B, H, N), dtype, d, causal, persistent launch
-    ((2, 40, 1000), torch.bfloat16, 128, False, True),  # RAGGED: partial last tile
+    ((2, 64, 1000), torch.bfloat16, 128, False, True),  # RAGGED: partial last tile
+    ((2, 40, 1000), torch.bfloat16, 128, False, False), # 1.25 rounds of 256-query blocks: 128-query tile
     ((1, 8, 1024), torch.float16, 128, False, True),    # small grid: 128-query tile, persistent
     ((1, 8, 1000), torch.bfloat16, 128, False, False),  # small grid: 128-query tile, last tile partial
     ((2, 8, 4032), torch.bfloat16, 64, False, True),    # RAGGED: 63 full tiles, padded to 64
@@ -887,14 +891,37 @@ def test_small_grid_tile_matches_the_256_query_tile(n, heads, dtype, out_dtype, 
     code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
     od = code if out_dtype is None else _native.DTYPE_F32
     desc_small = _native.fused_tc_kernel(code, od, heads, n, 128, causal)
-    desc_big = _native.fused_tc_kernel(code, od, 384, n, 128, causal)
+    desc_big = _native.fused_tc_kernel(code, od, 512, n, 128, causal)
     print(f"[small grid] n={n} heads={heads} {dtype} causal={causal}: {desc_small} / {desc_big}", flush=True)
     assert "BM=128" in desc_small and "BM=256" in desc_big
-    q, k, v = make_qkv(1, 384, n, 128, dtype, seed=44, device="cuda")
+    q, k, v = make_qkv(1, 512, n, 128, dtype, seed=44, device="cuda")
     big = cuda_attn.fused_tc(q, k, v, causal, out_dtype=out_dtype)[:, :heads]
     small = cuda_attn.fused_tc(*(t[:, :heads].contiguous() for t in (q, k, v)), causal, out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert torch.equal(small, big)
+
+
+@pytest.mark.parametrize("n, heads, dtype, out_dtype", [
+    (1024, 72, torch.bfloat16, None), (4000, 20, torch.bfloat16, torch.float32), (960, 80, torch.float16, None),
+    (1024, 144, torch.float16, torch.float32)])
+def test_mid_grid_tile_matches_the_256_query_tile(n, heads, dtype, out_dtype):
+    """d = 128 non-causal, more than one round of 256-query blocks (one per CU) with the last round
+    at most 85 % full: the 128-query tile, whose bits match those of the same heads in a batch that
+    fills whole rounds of the 256-query tile."""
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    od = code if out_dtype is None else _native.DTYPE_F32
+    blocks = (n + 255) // 256 * heads
+    rounds = (blocks + 255) // 256
+    assert rounds > 1 and 100 * (256 * rounds - blocks) >= 15 * 256 * rounds
+    desc_mid = _native.fused_tc_kernel(code, od, heads, n, 128)
+    desc_big = _native.fused_tc_kernel(code, od, 512, n, 128)
+    print(f"[mid grid] n={n} heads={heads} {dtype}: {desc_mid} / {desc_big}", flush=True)
+    assert "BM=128" in desc_mid and "BM=256" in desc_big
+    q, k, v = make_qkv(1, 512, n, 128, dtype, seed=45, device="cuda")
+    big = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)[:, :heads]
+    mid = cuda_attn.fused_tc(*(t[:, :heads].contiguous() for t in (q, k, v)), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(mid, big)
 
 
 def f64_rows_gpu(q, k, v, head, rows, causal):
