@@ -225,6 +225,13 @@ def test_fused_tc_kernel_description_without_gpu():
     d64 = _native.fused_tc_kernel(f16, f32, 128, 1024, 64)
     assert "D=64, BM=128" in d64 and "out f32" in d64 and "grid 1024 x 256 threads" in d64
     assert "key split 2" in _native.fused_tc_kernel(f16, f16, 42, 128, 64)
+    # d = 128, 256-query blocks (one per CU at a time, 256 CUs): the 128-query tile up to half the
+    # CUs (causal: all), and non-causal past one round where the last round is at most 85 % full
+    tile = lambda bh, n, causal=0: re.search(r"BM=(\d+)", _native.fused_tc_kernel(bf16, bf16, bh, n, 128, causal))[1]
+    assert [tile(32, 1024), tile(64, 1024), tile(64, 1024, 1), tile(80, 1024, 1)] == ["128", "256", "128", "256"]
+    assert [tile(72, 1024), tile(20, 4096), tile(144, 1024), tile(36, 4096)] == ["128"] * 4   # rounds 1.13-2.25
+    assert [tile(112, 1024), tile(64, 2048), tile(56, 4096), tile(128, 4096)] == ["256"] * 4  # rounds 1.75, 2, 3.5, 8
+    assert tile(72, 1024, 1) == "256"
     assert _native.fused_tc_kernel(f16, f16, 1, 64, 96) == ""
     assert _native.fused_tc_kernel(f32, f32, 1, 64, 64) == ""
     prev = _native.set_persistent(False)
