@@ -28,8 +28,11 @@ namespace pa {
 // column) is a different one. Grids are flattened into x: N rows times column blocks.
 
 // S[h][i][j0 + lane] for the wave's query row i and 64 keys from j0; keys after i are -inf when
-// causal.
-template <typename T>
+// causal. PIECES (rows of whole 16-byte pieces, 16-byte aligned): each lane reads its K row, and
+// the wave its Q row, a 16-byte piece per load instead of an element per load (one load then
+// touches the wave's 64 K rows once per piece, not once per element); the products are summed in
+// the same order either way.
+template <typename T, bool PIECES>
 __global__ void __launch_bounds__(256)
 naive_scores(const T* __restrict__ Q, const T* __restrict__ K, float* __restrict__ S, int N, int d,
              float scale, int causal, int key_blocks) {
@@ -38,12 +41,35 @@ naive_scores(const T* __restrict__ Q, const T* __restrict__ K, float* __restrict
   const int j = (unit % key_blocks) * kWave + (int)threadIdx.x % kWave;
   if (i >= N || j >= N) return;
   const size_t head = (size_t)blockIdx.y * N;
+  float* srow = S + (head + i) * N;
+  if (causal && j > i) {   // masked: the product is not needed
+    srow[j] = -INFINITY;
+    return;
+  }
   const T* qi = Q + (head + i) * d;
   const T* kj = K + (head + j) * d;
   float dot = 0.f;
-  for (int c = 0; c < d; ++c) dot = fmaf(to_f32(qi[c]), to_f32(kj[c]), dot);
-  float* srow = S + (head + i) * N;
-  srow[j] = (causal && j > i) ? -INFINITY : scale * dot;
+  if constexpr (PIECES) {
+    constexpr int E = 16 / (int)sizeof(T);   // elements per piece
+    for (int c = 0; c < d; c += E) {
+      // (the loaded vector is bit-cast as a whole before its elements are taken)
+      const u32x4 qw = *reinterpret_cast<const u32x4*>(qi + c);
+      const u32x4 kw = *reinterpret_cast<const u32x4*>(kj + c);
+      if constexpr (sizeof(T) == 4) {
+        const f32x4 qv = __builtin_bit_cast(f32x4, qw), kv = __builtin_bit_cast(f32x4, kw);
+#pragma unroll
+        for (int e = 0; e < E; ++e) dot = fmaf(qv[e], kv[e], dot);
+      } else {
+        const typename vec8<T>::type qv = __builtin_bit_cast(typename vec8<T>::type, qw);
+        const typename vec8<T>::type kv = __builtin_bit_cast(typename vec8<T>::type, kw);
+#pragma unroll
+        for (int e = 0; e < E; ++e) dot = fmaf(to_f32(qv[e]), to_f32(kv[e]), dot);
+      }
+    }
+  } else {
+    for (int c = 0; c < d; ++c) dot = fmaf(to_f32(qi[c]), to_f32(kj[c]), dot);
+  }
+  srow[j] = scale * dot;
 }
 
 // Row r of S in place: max, sum of exp(s - max), then exp(s - max) / sum, each a strided pass
@@ -65,8 +91,9 @@ naive_softmax(float* __restrict__ S, int N, long long rows) {
 }
 
 // O[h][i][c0 + lane] = sum over keys j of P[h][i][j] V[h][j][c0 + lane], for the wave's row i and
-// 64 head dims from c0.
-template <typename T>
+// 64 head dims from c0. PIECES (N a multiple of 4, P 16-byte aligned): the wave reads its P row
+// four probabilities per load; the products are summed in the same order either way.
+template <typename T, bool PIECES>
 __global__ void __launch_bounds__(256)
 naive_pv(const float* __restrict__ P, const T* __restrict__ V, T* __restrict__ O, int N, int d, int dim_blocks) {
   const int unit = (int)blockIdx.x * 4 + (int)threadIdx.x / kWave;   // (query row, 64-dim block)
@@ -77,7 +104,15 @@ naive_pv(const float* __restrict__ P, const T* __restrict__ V, T* __restrict__ O
   const float* pi = P + (head + i) * N;
   const T* vc = V + head * d + c;
   float acc = 0.f;
-  for (int j = 0; j < N; ++j) acc = fmaf(pi[j], to_f32(vc[(size_t)j * d]), acc);
+  if constexpr (PIECES) {
+    for (int j = 0; j < N; j += 4) {
+      const f32x4 p4 = *reinterpret_cast<const f32x4*>(pi + j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fmaf(p4[e], to_f32(vc[(size_t)(j + e) * d]), acc);
+    }
+  } else {
+    for (int j = 0; j < N; ++j) acc = fmaf(pi[j], to_f32(vc[(size_t)j * d]), acc);
+  }
   O[(head + i) * d + c] = from_f32<T>(acc);
 }
 

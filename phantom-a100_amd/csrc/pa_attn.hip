@@ -374,10 +374,15 @@ hipError_t launch_naive(const void* q, const void* k, const void* v, void* o, fl
   const long long rows = (long long)n * bh;
   if (score_units > INT_MAX - 4 || pv_units > INT_MAX - 4 || (rows + 3) / 4 > INT_MAX)   // 32-bit unit indices
     return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL(pa::naive_scores<T>, dim3((unsigned)((score_units + 3) / 4), bh), dim3(256), 0, stream,
+  // Rows of whole 16-byte pieces, 16-byte aligned: the scores read them a piece per load.
+  const bool pieces = d * (int)sizeof(T) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(k) % 16 == 0;
+  auto scores = pieces ? pa::naive_scores<T, true> : pa::naive_scores<T, false>;
+  hipLaunchKernelGGL(scores, dim3((unsigned)((score_units + 3) / 4), bh), dim3(256), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k), s, n, d, scale, causal, (int)key_blocks);
   hipLaunchKernelGGL(pa::naive_softmax, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, s, n, rows);
-  hipLaunchKernelGGL(pa::naive_pv<T>, dim3((unsigned)((pv_units + 3) / 4), bh), dim3(256), 0, stream, s,
+  auto pv = n % 4 == 0 && reinterpret_cast<uintptr_t>(s) % 16 == 0 ? pa::naive_pv<T, true> : pa::naive_pv<T, false>;
+  hipLaunchKernelGGL(pv, dim3((unsigned)((pv_units + 3) / 4), bh), dim3(256), 0, stream, s,
                      static_cast<const T*>(v), static_cast<T*>(o), n, d, (int)dim_blocks);
   return hipGetLastError();
 }
