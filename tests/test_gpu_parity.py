@@ -198,6 +198,42 @@ def test_other_head_dims_for_unfused(name, d, causal):
     assert max_err(out.double(), f64_reference_gpu(q, k, v, causal)) <= F32_BAR
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_naive_piece_loads_match_element_loads(dtype, causal):
+    """naive reads Q and K rows a 16-byte piece per load when they are 16-byte aligned and hold
+    whole pieces, and the P rows four probabilities per load when the workspace is aligned and
+    N % 4 == 0; otherwise an element per load. The products are summed in the same order either
+    way, so inputs (and a workspace) one element off alignment give the same bits."""
+    b, h, n, d = 1, 3, 260, 64
+    code = {torch.float32: _native.DTYPE_F32, torch.float16: _native.DTYPE_F16}[dtype]
+    q, k, v = make_qkv(b, h, n, d, dtype, seed=9, device="cuda")
+
+    def shifted(t):   # the same values, contiguous, one element past a 16-byte boundary
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device="cuda")
+        out = buf[1:].view(t.shape)
+        out.copy_(t)
+        return out
+
+    def naive(q_, k_, v_, s_):
+        o = torch.empty_like(q_)
+        rc = _native.lib().pa_naive_fwd(q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), s_.data_ptr(),
+                                        code, b * h, n, d, int(causal), torch.cuda.current_stream().cuda_stream)
+        _native.check(rc, "naive_forward")
+        return o
+
+    s = torch.empty(b * h * n * n, dtype=torch.float32, device="cuda")
+    s_off = shifted(s)
+    qs, ks, vs = shifted(q), shifted(k), shifted(v)
+    assert qs.data_ptr() % 16 and s_off.data_ptr() % 16 and qs.is_contiguous()
+    want = naive(q, k, v, s)   # piece loads in both kernels
+    got_in = naive(qs, ks, vs, s)   # element loads for the scores
+    got_ws = naive(q, k, v, s_off)   # element loads for P.V
+    torch.cuda.synchronize()
+    assert torch.equal(got_in, want) and torch.equal(got_ws, want)
+    assert torch.equal(want, cuda_attn.naive(q, k, v, causal))
+
+
 def f64_rows(q, k, v, rows, causal):
     """float64 softmax(QK^T/sqrt(d))V for the given query rows of every head."""
     b, h, n, d = q.shape
