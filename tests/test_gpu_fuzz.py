@@ -99,3 +99,40 @@ def test_random_shape_matches_float64(case):
     bar += 0.5 * torch.finfo(want_dtype).eps * ref.abs().max().item()
     err = (out.double() - ref).abs().max().item()
     assert np.isfinite(err) and err <= bar, f"{case_id(c)}: max abs error {err:.3e} > {bar:.3e}"
+
+
+def draw_grid_cases(count: int = 24, seed: int = 2027):
+    """fused_tc on grids of 100-900 heads: the persistent walks, the d = 128 128-query tile where
+    the last round of 256-query blocks is far from full, and the causal lists, at shapes between
+    the fixed ones."""
+    rng = random.Random(seed)
+    cases = []
+    for i in range(count):
+        b = rng.randint(1, 4)
+        h = max(1, rng.randint(100, 900) // b)
+        n = max(2, int(round(math.exp(rng.uniform(math.log(64), math.log(3000))))))
+        cases.append(dict(name="fused_tc", b=b, h=h, n=n, d=rng.choice((64, 128)),
+                          dtype=rng.choice((torch.float16, torch.bfloat16)), causal=rng.random() < 0.5,
+                          out_dtype=torch.float32 if rng.random() < 0.4 else None, kw={}, seed=5000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", draw_grid_cases(), ids=case_id)
+def test_many_heads_match_float64_on_sampled_heads(case):
+    c = case
+    b, h, n, d = c["b"], c["h"], c["n"], c["d"]
+    print(f"[fuzz grid] {case_id(c)}", flush=True)
+    q, k, v = make_qkv(b, h, n, d, c["dtype"], seed=c["seed"], device="cuda")
+    out = cuda_attn.fused_tc(q, k, v, c["causal"], out_dtype=c["out_dtype"])
+    want_dtype = c["out_dtype"] or c["dtype"]
+    assert out.shape == q.shape and out.dtype == want_dtype
+    heads = sorted({0, random.Random(c["seed"]).randrange(b * h), b * h - 1})
+    qh, kh, vh = (t.reshape(1, b * h, n, d)[:, heads].contiguous() for t in (q, k, v))
+    ref = f64_reference(qh, kh, vh, c["causal"])
+    bar = 2e-3
+    if c["dtype"] == torch.bfloat16:
+        qn, kn, vn = (t[0].float().cpu().numpy() for t in (qh, kh, vh))
+        bar, _, _ = pb.reference_bar(qn, kn, vn, c["causal"], torch.bfloat16, ref[0].cpu().numpy())
+    bar += 0.5 * torch.finfo(want_dtype).eps * ref.abs().max().item()
+    err = (out.reshape(1, b * h, n, d)[:, heads].double() - ref).abs().max().item()
+    assert np.isfinite(err) and err <= bar, f"{case_id(c)}: max abs error {err:.3e} > {bar:.3e}"
