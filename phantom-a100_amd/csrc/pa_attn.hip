@@ -292,9 +292,10 @@ bool use_key_split(int64_t d, int64_t n, int64_t bh, int causal) {
   const int64_t blocks = (n + 127) / 128 * bh;
   return (n <= 256 && (n + 63) / 64 * bh <= kCUs) || blocks <= kCUs / 2 || (causal && n >= 4096 && blocks <= kCUs);
 }
-// Small grids at d = 128: 128-query workgroups (4 waves, two per CU) where the 256-query blocks
-// would fill at most half the CUs, so the work spreads over twice the CUs; every wave computes
-// exactly as in the 256-query tile (same bits). Measured back to back against the 256-query tile,
+// d = 128 grids the 256-query blocks would leave partly idle: 128-query workgroups (4 waves, two
+// per CU) where those blocks fill at most half the CUs (causal: at most all), so the work spreads
+// over twice the CUs, and non-causal past one round where the last round is far from full. Every
+// wave computes exactly as in the 256-query tile (same bits). Measured back to back against it,
 // TFLOP/s, non-causal bf16: 1x8x1024 176 -> 234, 1x16x1024 356 -> 458, 1x32x1024 687 -> 813,
 // 1x16x2048 833 -> 954, 1x4x4096 467 -> 629, 2x8x2048 813 -> 948, 1x2x8192 489 -> 654, 1x64x512
 // 534 -> 652; causal: bf16 1x8x2048 203 -> 277, 1x16x1024 171 -> 222, 1x4x4096 227 -> 322, 1x8x1000
