@@ -309,7 +309,12 @@ bool use_key_split(int64_t d, int64_t n, int64_t bh, int causal) {
 // 1180, 5x16x2048 (2.5) 1108 -> 1163, 1x80x2048 (2.5) 1119 -> 1171; fp16 1x24x4096 (1.5) 1055 ->
 // 1100, 1x144x1024 (2.25) 822 -> 910; and loses where it is nearly full or full: 1x112x1024 (1.75)
 // 1005 -> 950, 1x56x4096 (3.5) 1216 -> 1221, 2x32x2048 (2) 1128 -> 1068, C4 (8) 1290 -> 1195.
-// Causal rows beyond one round lost with it (3x32x2048 970 -> 863, 1x40x4096 1070 -> 975).
+// Causal rows beyond one round lost with it (3x32x2048 970 -> 863, 1x40x4096 1070 -> 975). Where
+// a row's last 256-query block is mostly padding, the 128-query tile computes fewer rows: non-causal
+// bf16 past one round 4x256x128 263 -> 371, 1x512x384 659 -> 774, 2x128x896 976 -> 1033, fp16
+// 2x256x640 833 -> 896; 1x256x1100 (11 % padding) 946 -> 946, 1x256x1536 (none) 1137 -> 1071;
+// within one round 1x256x128 233 -> 270, 1x200x100 107 -> 127, but 1x100x384 500 -> 474 and
+// 1x40x1100 754 -> 693.
 const MfmaEntry kTcSmallGridTable[] = {
     PA_TC_BOTH_OUT(pa::f16, 128, 128, 64, 2),
     PA_TC_BOTH_OUT(pa::bf16, 128, 128, 64, 2),
@@ -319,9 +324,14 @@ bool use_small_grid_tile(int64_t d, int64_t n, int64_t bh, int causal) {
   const int64_t blocks = (n + 255) / 256 * bh;   // 256-query blocks, one workgroup per CU at a time
   if (causal) return blocks <= kCUs;
   if (blocks <= kCUs / 2) return true;
-  if (blocks <= kCUs) return false;
-  // More than one round of 256-query blocks: the 128-query tile where the last round would leave at
-  // least 15 % of the launch's CU time idle (its half-size blocks fill that round's CUs better).
+  // Rows of a head computed by each tile: a row's last block is padded to the tile (rows past N
+  // are computed and not stored).
+  const int64_t rows256 = (n + 255) / 256 * 256, rows128 = (n + 127) / 128 * 128;
+  if (blocks <= kCUs) return n <= 128;   // one round: where half of every 256-query block is padding
+  // More than one round of 256-query blocks: the 128-query tile where at least 14 % of the
+  // 256-query tile's rows are padding, or where its last round would leave at least 15 % of the
+  // launch's CU time idle (the half-size blocks fill that round's CUs better).
+  if (100 * rows256 >= 114 * rows128) return true;
   const int64_t rounds = (blocks + kCUs - 1) / kCUs, last = blocks - (rounds - 1) * kCUs;
   return 100 * (kCUs - last) >= 15 * rounds * kCUs;
 }

@@ -160,7 +160,8 @@ def fused_tc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = F
     key split instead where the grid is small (rows of 2-4 key tiles, or 128-query blocks that fill
     at most half the CUs), and at d = 128 where the 256-query blocks would fill at most half the
     CUs (causal: at most all of them) or, non-causal, leave the last round of one block per CU at
-    most 85 % full, 128-query workgroups (same bits); otherwise one workgroup per query block.
+    most 85 % full or hold mostly padding rows (N <= 128, or past one round at least 14 % of the
+    rows), 128-query workgroups (same bits); otherwise one workgroup per query block.
     cuda_attn._native.fused_tc_kernel names the launch a call takes. PA_PERSISTENT=0 in the
     environment when the library loads, or cuda_attn._native.set_persistent(False), selects one
     workgroup per query block instead of the persistent launch (same bits, except for fp16 at d = 64

@@ -232,6 +232,10 @@ def test_fused_tc_kernel_description_without_gpu():
     assert [tile(72, 1024), tile(20, 4096), tile(144, 1024), tile(36, 4096)] == ["128"] * 4   # rounds 1.13-2.25
     assert [tile(112, 1024), tile(64, 2048), tile(56, 4096), tile(128, 4096)] == ["256"] * 4  # rounds 1.75, 2, 3.5, 8
     assert tile(72, 1024, 1) == "256"
+    # rows whose last 256-query block is mostly padding: past one round from 14 % padding on
+    # (N = 128, 384, 896), within one round for N <= 128 only
+    assert [tile(600, 128), tile(512, 384), tile(256, 896), tile(256, 128)] == ["128"] * 4
+    assert [tile(256, 1100), tile(100, 384), tile(40, 1100), tile(256, 1536)] == ["256"] * 4
     assert _native.fused_tc_kernel(f16, f16, 1, 64, 96) == ""
     assert _native.fused_tc_kernel(f32, f32, 1, 64, 64) == ""
     prev = _native.set_persistent(False)

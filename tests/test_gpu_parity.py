@@ -551,12 +551,12 @@ PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype; d = 128
     ((1, 304, 128), torch.float16, 1.0, torch.float32),
     ((2, 40, 1024), torch.float16, 10.0, torch.float32),
     ((2, 64, 1000), torch.bfloat16, 1.0, None),          # ragged: last tile 40 keys
-    ((1, 160, 100), torch.bfloat16, 3.0, torch.float32), # ragged, two tiles
+    ((1, 160, 200), torch.bfloat16, 3.0, torch.float32), # ragged, four tiles
     ((4, 32, 4032), torch.bfloat16, 1.0, None),          # 63 full tiles, padded to 64
     ((2, 64, 960), torch.float16, 3.0, torch.float32),   # 15 full tiles
     ((1, 160, 192), torch.bfloat16, 10.0, torch.float32), # 3 tiles, rescaling rows
     ((2, 64, 1000), torch.float16, 1.0, torch.float32),
-    ((1, 160, 100), torch.float16, 3.0, None),
+    ((1, 160, 200), torch.float16, 3.0, None),
     # small grids (256-query blocks filling at most half the CUs): the 128-query tile, two
     # workgroups per CU
     ((1, 8, 2048), torch.bfloat16, 1.0, None),
@@ -567,10 +567,10 @@ PERSISTENT_SHAPES = [  # (B, H, N), dtype, qk_scale, out dtype; d = 128
     ((1, 20, 4096), torch.float16, 1.0, torch.float32),
     ((4, 32, 4050), torch.bfloat16, 1.0, None),          # ragged, 2048 blocks: 8 per workgroup
     ((16, 16, 1000), torch.bfloat16, 1.0, torch.float32),  # ragged, 1024 blocks
-    ((1, 752, 100), torch.bfloat16, 3.0, None),          # ragged, two tiles, 752 blocks
+    ((1, 752, 200), torch.bfloat16, 3.0, None),          # ragged, four tiles, 752 blocks
     ((4, 32, 4050), torch.float16, 1.0, torch.float32),
     ((16, 16, 1000), torch.float16, 1.0, None),
-    ((1, 752, 100), torch.float16, 3.0, torch.float32),
+    ((1, 752, 200), torch.float16, 3.0, torch.float32),
 ]
 
 
@@ -918,7 +918,7 @@ def test_key_split_on_small_grids(n, heads, dtype, causal):
 
 @pytest.mark.parametrize("n, heads, dtype, out_dtype", [
     (2048, 8, torch.bfloat16, None), (1024, 16, torch.float16, torch.float32), (1000, 8, torch.bfloat16, None),
-    (1030, 4, torch.float16, None), (8192, 1, torch.float16, torch.float32), (100, 40, torch.bfloat16, None)])
+    (1030, 4, torch.float16, None), (8192, 1, torch.float16, torch.float32), (200, 40, torch.bfloat16, None)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_small_grid_tile_matches_the_256_query_tile(n, heads, dtype, out_dtype, causal):
     """d = 128, 256-query blocks filling at most half the CUs: the 128-query tile (two workgroups
@@ -958,6 +958,29 @@ def test_mid_grid_tile_matches_the_256_query_tile(n, heads, dtype, out_dtype):
     mid = cuda_attn.fused_tc(*(t[:, :heads].contiguous() for t in (q, k, v)), out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert torch.equal(mid, big)
+
+
+@pytest.mark.parametrize("n, heads, dtype, out_dtype", [
+    (128, 600, torch.bfloat16, None), (384, 512, torch.float16, torch.float32), (896, 256, torch.bfloat16, None),
+    (100, 300, torch.bfloat16, torch.float32), (128, 256, torch.float16, None)])
+def test_padded_rows_take_the_128_query_tile(n, heads, dtype, out_dtype):
+    """d = 128 non-causal rows whose last 256-query block would be mostly padding (rows past N are
+    computed and not stored): the 128-query tile, past one round of 256-query blocks from 14 %
+    padding on and within one round for N <= 128. Sampled heads against float64."""
+    code = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}[dtype]
+    od = code if out_dtype is None else _native.DTYPE_F32
+    desc = _native.fused_tc_kernel(code, od, heads, n, 128)
+    print(f"[padded rows] n={n} heads={heads} {dtype}: {desc}", flush=True)
+    assert "BM=128" in desc
+    q, k, v = make_qkv(1, heads, n, 128, dtype, seed=46, device="cuda")
+    out = cuda_attn.fused_tc(q, k, v, out_dtype=out_dtype)
+    sel = sorted({0, heads // 3, heads - 1})
+    qh, kh, vh = (t[:, sel].contiguous() for t in (q, k, v))
+    ref = f64_reference_gpu(qh, kh, vh)
+    qn, kn, vn = (t[0].float().cpu().numpy() for t in (qh, kh, vh))
+    tol, _, _ = pb.reference_bar(qn, kn, vn, False, dtype, ref[0].cpu().numpy())
+    tol += 0.5 * torch.finfo(out.dtype).eps * ref.abs().max().item()
+    assert max_err(out[:, sel], ref) <= tol
 
 
 def f64_rows_gpu(q, k, v, head, rows, causal):
