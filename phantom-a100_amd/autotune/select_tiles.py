@@ -202,10 +202,25 @@ def evaluate(args) -> list[dict]:
     comp = compulsory_bytes(args.batch * args.heads, args.n, args.dim, dt, dt)
     rows = []
     only = set(args.only.split(",")) if args.only else None
+    bh = args.batch * args.heads
+    # An alternative whose launch is the shipped one is skipped where the shipped row is evaluated too.
+    shipped = ""
+    if args.entry == "fused_tc":
+        sbr, sbc, sst = TC_TILE[args.dim]
+        if only is None or f"br{sbr}_bc{sbc}_{sst}stage" in only:
+            shipped = launch_form(args.entry, dt, args.dim, args.n, bh, args.causal, sbr, SHIPPED)["description"]
     for label, br, bc, st, source in candidates(args.entry, args.dim, dt, with_alternatives=not args.shipped_only):
         if only is not None and label not in only:
             continue
+        form = launch_form(args.entry, dt, args.dim, args.n, bh, args.causal, br, source)
+        if source in (SHIPPED, PER_BLOCK) and form.get("tile") and form["tile"] != (br, bc, st):
+            # fused_tc launches another tile on this grid: the row names the tile that runs
+            tb, tn, ts = form["tile"]
+            label = f"br{tb}_bc{tn}_{ts}stage{'_per_block' if source == PER_BLOCK else ''} (as launched)"
         row = {"candidate": label, "br": br, "bc": bc, "stages": st}
+        if isinstance(source, int) and shipped and form["description"] == shipped:
+            rows.append(dict(row, status="skipped: the shipped launch"))
+            continue
         fn = make_call(args.entry, q, k, v, args.causal, br, bc, st, source=source)
         try:   # gate on fp32 output where the candidate has one, so the 2e-3 bar does not include
             # the output's own rounding; the alternatives (input-dtype output) get that rounding on top
@@ -221,7 +236,6 @@ def evaluate(args) -> list[dict]:
             continue
         med, p10, p90 = time_calls(fn, 5, args.iters, flush)
         row.update(status="ok", median_ms=med, p10_ms=p10, p90_ms=p90, tflops=flops / (med * 1e-3) / 1e12)
-        form = launch_form(args.entry, dt, args.dim, args.n, args.batch * args.heads, args.causal, br, source)
         kbr, kbc, kst = form.get("tile") or (br, bc, st)
         res = find_resources(res_all, kernel_key(dt, args.dim, kbr, kbc, kst, dt, form["ksplit"], form["persistent"],
                                                  form["ragged"], form["causal"], form["check"]))
@@ -234,7 +248,7 @@ def evaluate(args) -> list[dict]:
             row["resident_wgs_per_cu"] = dg.resident_wgs_per_cu(waves, threads)
         row["workgroups"] = form["workgroups"]
         if args.profile and args.profile_dir:      # keep the raw rocprofv3 output per candidate
-            prof = profile_candidate(args, br, bc, st, os.path.join(args.profile_dir, label), source, label)
+            prof = profile_candidate(args, br, bc, st, os.path.join(args.profile_dir, label.split()[0]), source, label)
         elif args.profile:
             with tempfile.TemporaryDirectory() as tmp:
                 prof = profile_candidate(args, br, bc, st, tmp, source, label)

@@ -86,6 +86,9 @@ const Candidate kCandidates[] = {
     PA_CAND("br256_bc32_2stage_persistent", pa::bf16, PA_DTYPE_BF16, 128, 256, 32, 2, true, 0),
     PA_CAND("br256_bc128_1stage", pa::bf16, PA_DTYPE_BF16, 128, 256, 128, 1, false, 0),
     PA_CAND("br256_bc64_1stage", pa::bf16, PA_DTYPE_BF16, 128, 256, 64, 1, false, 0),
+    // fused_tc's general d = 128 tile, persistent: the alternative on the grids where fused_tc
+    // launches the 128-query tile (a grid where fused_tc launches this one skips it as a duplicate)
+    PA_CAND("br256_bc64_2stage_persistent_d128", pa::bf16, PA_DTYPE_BF16, 128, 256, 64, 2, true, 0),
     PA_CAND("br256_bc64_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 256, 64, 2, true, 0),
     PA_CAND("br64_bc64_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 64, 64, 2, true, 0),
     PA_CAND("br128_bc32_2stage_persistent", pa::f16, PA_DTYPE_F16, 64, 128, 32, 2, true, 0),
