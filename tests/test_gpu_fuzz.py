@@ -136,3 +136,41 @@ def test_many_heads_match_float64_on_sampled_heads(case):
     bar += 0.5 * torch.finfo(want_dtype).eps * ref.abs().max().item()
     err = (out.reshape(1, b * h, n, d)[:, heads].double() - ref).abs().max().item()
     assert np.isfinite(err) and err <= bar, f"{case_id(c)}: max abs error {err:.3e} > {bar:.3e}"
+
+
+def draw_walk_cases(count: int = 24, seed: int = 2028):
+    """Shapes for the persistent walks against one workgroup per query block, in the dtypes where
+    the two launches compute every row alike: bf16 and fp16 d = 128, and causal fp16 d = 64 (fp16
+    d = 64 non-causal starts a rescale on a different rule per launch)."""
+    rng = random.Random(seed)
+    cases = []
+    for i in range(count):
+        b = rng.randint(1, 4)
+        h = max(1, rng.randint(1, 900) // b)
+        n = int(round(math.exp(rng.uniform(math.log(100), math.log(4096)))))   # at least two key tiles
+        d, causal = rng.choice((64, 128)), rng.random() < 0.5
+        dtype = rng.choice((torch.float16, torch.bfloat16)) if d == 128 or causal else torch.bfloat16
+        cases.append(dict(name="fused_tc", b=b, h=h, n=n, d=d, dtype=dtype, causal=causal,
+                          out_dtype=torch.float32 if rng.random() < 0.4 else None, kw={}, seed=7000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", draw_walk_cases(), ids=case_id)
+def test_persistent_walk_matches_per_block_launch_on_every_head(case):
+    """fused_tc's persistent launch (workgroups walking the query blocks of their XCD, or the causal
+    lists) against one workgroup per query block, bit for bit over the whole output: a block that a
+    walk skipped, visited twice or handed a wrong head would show in some row of some head."""
+    from cuda_attn import _native
+    c = case
+    print(f"[fuzz walk] {case_id(c)}", flush=True)
+    q, k, v = make_qkv(c["b"], c["h"], c["n"], c["d"], c["dtype"], seed=c["seed"], device="cuda")
+    prev = _native.set_persistent(True)
+    try:
+        got = cuda_attn.fused_tc(q, k, v, c["causal"], out_dtype=c["out_dtype"])
+        _native.set_persistent(False)
+        want = cuda_attn.fused_tc(q, k, v, c["causal"], out_dtype=c["out_dtype"])
+    finally:
+        _native.set_persistent(prev)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want)
