@@ -152,6 +152,13 @@ def draw_walk_cases(count: int = 24, seed: int = 2028):
         dtype = rng.choice((torch.float16, torch.bfloat16)) if d == 128 or causal else torch.bfloat16
         cases.append(dict(name="fused_tc", b=b, h=h, n=n, d=d, dtype=dtype, causal=causal,
                           out_dtype=torch.float32 if rng.random() < 0.4 else None, kw={}, seed=7000 + i))
+    # many heads of short rows: every workgroup walks tens of blocks
+    for i, (h, n, d, dtype, causal) in enumerate(((20000, 130, 128, torch.bfloat16, False),
+                                                  (12000, 300, 128, torch.float16, True),
+                                                  (30000, 200, 64, torch.bfloat16, False),
+                                                  (16000, 256, 64, torch.float16, True))):
+        cases.append(dict(name="fused_tc", b=1, h=h, n=n, d=d, dtype=dtype, causal=causal, out_dtype=None, kw={},
+                          seed=7100 + i))
     return cases
 
 
