@@ -721,8 +721,8 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
           // favours a wave starting its S(t+1) MFMAs over the other waves' phase B. Measured back
           // to back against priority 0 throughout (bits unchanged): C4 +0.4-0.9 %, C3 +2.4-2.6 %,
           // C5 +1.0-1.8 %, fp16 4x32x4096 d = 128 +0.5-2.7 %, bf16 8x16x2048 d = 64 +2.5 %, causal
-          // C4 +0.5 %; priority 1 or 3 within 0.2 % of 2; priority raised for phase B instead lost
-          // 0.4-0.9 % at d = 64.
+          // C4 +0.5 %, the bf16 key split on causal 1x5x4096 +4 %; priority 1 or 3 within 0.2 % of
+          // 2; priority raised for phase B instead lost 0.4-0.9 % at d = 64.
           __builtin_amdgcn_s_setprio(2);
           qk(sn, kn);
           // This iteration's tile loads, issued inside phase A (unconditionally, to keep the phase
@@ -990,6 +990,9 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
             // C5 +0.6 % over the per-phase totals 5 and 11, within 1 % for 4-6 and 4-11)
             constexpr int VA = (D == 64 && BM == 128 && BN == 64 && !RS)
                                    ? 4 : ((PV_STEPS - QB) * 20 + (RS ? NDB * 16 + 2 : 0) + QK_MFMAS - 1) / QK_MFMAS;
+            // Phase A at wave priority 2, as on the bf16 path (causal fp16 d = 64 4x16x1024 +2.1-3.1 %,
+            // 1x16x2048 +1.0-1.2 %); not in the key split, which lost 8 % with it (C2, 1x4x8192).
+            if constexpr (KSPLIT == 1) __builtin_amdgcn_s_setprio(2);
             qk(sn, kn);
             if constexpr (RS) rescale_o(alpha);
             exp_part(s, pf, QB, PV_STEPS, true);
@@ -1002,6 +1005,7 @@ fa_mfma_fwd(const T* __restrict__ Q, const T* __restrict__ K, const T* __restric
               __builtin_amdgcn_sched_group_barrier(kSchedValu, VA, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (KSPLIT == 1) __builtin_amdgcn_s_setprio(0);
           };
           if (rescale) phase_a(std::true_type{});
           else phase_a(std::false_type{});
